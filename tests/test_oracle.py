@@ -1,0 +1,313 @@
+"""Pins the CPU oracle before anything is compared against it.
+
+Each restated function is checked against the reference's own known-answer tests
+(crates/jevons-formats/src/quant.rs:195-237, crates/jevons-core/src/model.rs:221-234), against a
+library routine where one exists (numpy/torch float conversions, numpy matmul), or against
+hand-built blocks whose decoded values follow from the block layout alone, so that a wrong
+index, shift, sign or dropped term fails one of them.
+"""
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+
+def f16_bytes(v: float) -> bytes:
+    return np.float16(v).tobytes()
+
+
+# ---------------------------------------------------------------- f16 / bf16 conversions
+
+def test_f16_to_f32_matches_numpy_for_all_65536_patterns(oracle):
+    pats = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = pats.view(np.float16).astype(np.float32)
+    got = np.array([oracle.f16_to_f32(int(p)) for p in pats], dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_rounds_to_nearest_even_like_numpy(oracle):
+    rng = np.random.default_rng(5)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(1e-3),
+        rng.standard_normal(20000).astype(np.float32) * np.float32(300.0),
+        (rng.random(5000).astype(np.float32) * np.float32(1e-6)),  # subnormal range
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e9, -1e9, 2.0 ** -24,
+                  2.0 ** -25, 2.0 ** -25 * 1.0000001, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11,
+                  np.inf, -np.inf], dtype=np.float32),
+    ])
+    with np.errstate(over="ignore"):
+        want = vals.astype(np.float16).view(np.uint16)
+    got = np.array([oracle.f32_to_f16(float(v)) for v in vals], dtype=np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_bf16_conversions_match_torch(oracle):
+    L = oracle.lib()
+    rng = np.random.default_rng(6)
+    vals = rng.standard_normal(5000).astype(np.float32) * np.float32(50.0)
+    want = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = np.array([L.jvo_f32_to_bf16(float(v)) for v in vals], dtype=np.uint16)
+    assert np.array_equal(got, want)
+    back = np.array([L.jvo_bf16_to_f32(int(h)) for h in want], dtype=np.float32)
+    assert np.array_equal(back, torch.from_numpy(want.view(np.int16)).view(torch.bfloat16).float().numpy())
+
+
+# ---------------------------------------------------------------- type table
+
+def test_type_table_matches_gguf_block_sizes(oracle):
+    # gguf.rs:134-144
+    assert oracle.type_block(0) == (1, 4)
+    assert oracle.type_block(1) == (1, 2)
+    assert oracle.type_block(6) == (32, 22)
+    assert oracle.type_block(8) == (32, 34)
+    assert oracle.type_block(12) == (256, 144)
+    assert oracle.type_block(14) == (256, 210)
+    for other in (2, 3, 7, 10, 11, 13, 15, 30):
+        assert oracle.type_block(other) is None
+    assert oracle.packed_words(12) == (36, 0, 0, 0)
+    assert oracle.packed_words(14) == (32, 16, 4, 1)
+    assert oracle.packed_words(6) == (4, 1, 0, 1)
+    assert oracle.packed_words(8) == (8, 0, 0, 1)
+
+
+# ---------------------------------------------------------------- reference KATs
+
+def test_q4k_decodes_scale_high_bits_for_upper_groups(oracle):
+    # quant.rs:199-208
+    q = bytes([0xc1, 0x82, 0x43, 0x04, 0x85, 0xc6, 0x07, 0x48, 0x12, 0x34, 0x56, 0x78])
+    pairs = [oracle.q4k_scale_min(j, q) for j in range(8)]
+    assert pairs[0] == (1, 5)
+    assert pairs[4] == (50, 33)
+    assert pairs[7] == (8, 23)
+
+
+def test_q8_0_and_q5_0_dequantize_signed_values(oracle):
+    # quant.rs:210-226
+    q8 = bytearray(34)
+    q8[0:2] = f16_bytes(0.5)
+    q8[2] = (-4) & 0xFF
+    q8[33] = 7
+    out = oracle.dequantize(oracle.Q8_0, np.frombuffer(bytes(q8), np.uint8))
+    assert (out[0], out[31]) == (-2.0, 3.5)
+
+    q5 = bytearray(22)
+    q5[0:2] = f16_bytes(1.0)
+    q5[2:6] = struct.pack("<I", 1 | (1 << 16))
+    q5[6] = 0x3F
+    out = oracle.dequantize(oracle.Q5_0, np.frombuffer(bytes(q5), np.uint8))
+    assert (out[0], out[16], out[1]) == (15.0, 3.0, -16.0)
+
+
+def test_packing_splits_quants_and_scales_without_changing_values(oracle):
+    # quant.rs:228-237
+    q8 = bytearray(34)
+    q8[0:2] = f16_bytes(0.5)
+    q8[2:6] = bytes([1, 2, 3, 4])
+    q, h, s, d = oracle.pack(oracle.Q8_0, np.frombuffer(bytes(q8), np.uint8))
+    assert len(q) == 8 and list(d) == [0.5]
+    assert q[0] == struct.unpack("<I", bytes([1, 2, 3, 4]))[0]
+    with pytest.raises(oracle.OracleError):
+        oracle.pack(oracle.Q8_0, np.frombuffer(bytes(q8[:33]), np.uint8))
+
+
+def test_greedy_takes_the_first_argmax_with_its_stable_probability(oracle):
+    # crates/jevons-core/src/model.rs:221-234
+    tok, conf = oracle.greedy(np.array([1000.0, 1000.0 + np.log(np.float32(2.0)), 0.0], np.float32))
+    assert tok == 1 and abs(conf - 2.0 / 3.0) < 1e-4
+    assert oracle.greedy(np.array([3.0, 3.0], np.float32))[0] == 0
+    with pytest.raises(oracle.OracleError):
+        oracle.greedy(np.array([np.inf], np.float32))
+    with pytest.raises(oracle.OracleError):
+        oracle.greedy(np.array([], np.float32))
+    with pytest.raises(oracle.OracleError):
+        oracle.greedy(np.array([1.0, np.nan], np.float32))
+
+
+def test_dequantize_rejects_bad_sizes_and_types(oracle):
+    with pytest.raises(oracle.OracleError, match="size mismatch"):
+        oracle.dequantize(oracle.Q4K, np.zeros(143, np.uint8), 256)
+    with pytest.raises(oracle.OracleError, match="size mismatch"):
+        oracle.dequantize(oracle.Q4K, np.zeros(144, np.uint8), 255)
+    with pytest.raises(oracle.OracleError, match="unsupported"):
+        oracle.dequantize(2, np.zeros(18, np.uint8), 32)
+    with pytest.raises(oracle.OracleError, match="no GPU block layout"):
+        oracle.pack(oracle.F16, np.zeros(4, np.uint8))
+
+
+# ---------------------------------------------------------------- hand-built Q4_K blocks
+
+def q4k_block(d, dmin, scales12, qs128):
+    return np.frombuffer(f16_bytes(d) + f16_bytes(dmin) + bytes(scales12) + bytes(qs128), np.uint8)
+
+
+def test_q4k_unit_scales_decode_to_the_raw_nibbles(oracle):
+    # scales 0..3 = 1 (bytes 0..3), mins 0 (bytes 4..7), scales 4..7 = 1 (low nibbles of 8..11)
+    scales = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]
+    qs = [(i * 7 + 3) & 0xFF for i in range(128)]
+    w = oracle.dequantize(oracle.Q4K, q4k_block(1.0, 0.0, scales, qs))
+    for p in range(4):
+        for l in range(32):
+            b = qs[32 * p + l]
+            assert w[64 * p + l] == (b & 15)
+            assert w[64 * p + 32 + l] == (b >> 4)
+
+
+def test_q4k_single_nibble_lands_at_its_element_with_its_sub_block_scale(oracle):
+    # KAT scale bytes give (scale, min) = (1,5) (2,6) (3,7) (4,8) (50,33) (36,51) (22,5) (8,23):
+    # j=5: (0x34&15)|((0x82>>6)<<4) = 36, (0x34>>4)|((0xc6>>6)<<4) = 51; j=6: 6|16 = 22, 5|0 = 5
+    scales = [0xc1, 0x82, 0x43, 0x04, 0x85, 0xc6, 0x07, 0x48, 0x12, 0x34, 0x56, 0x78]
+    pairs = [(1, 5), (2, 6), (3, 7), (4, 8), (50, 33), (36, 51), (22, 5), (8, 23)]
+    assert [oracle.q4k_scale_min(j, bytes(scales)) for j in range(8)] == pairs
+    d, dmin = 0.5, 0.25
+    for p, l, lo, hi in [(0, 0, 3, 0), (1, 17, 0, 9), (2, 31, 15, 15), (3, 5, 1, 2)]:
+        qs = [0] * 128
+        qs[32 * p + l] = lo | (hi << 4)
+        w = oracle.dequantize(oracle.Q4K, q4k_block(d, dmin, scales, qs))
+        want = np.array([-dmin * pairs[e // 32][1] for e in range(256)], np.float32)
+        want[64 * p + l] = d * pairs[2 * p][0] * lo - dmin * pairs[2 * p][1]
+        want[64 * p + 32 + l] = d * pairs[2 * p + 1][0] * hi - dmin * pairs[2 * p + 1][1]
+        assert np.array_equal(w, want), (p, l)
+
+
+def test_q4k_matches_a_vectorised_restatement_on_random_blocks(oracle):
+    rng = np.random.default_rng(7)
+    nb = 64
+    raw = rng.integers(0, 256, size=(nb, 144), dtype=np.uint8)
+    raw[:, 0:2] = np.frombuffer(np.abs(rng.standard_normal(nb)).astype(np.float16).tobytes(), np.uint8).reshape(nb, 2)
+    raw[:, 2:4] = np.frombuffer(np.abs(rng.standard_normal(nb)).astype(np.float16).tobytes(), np.uint8).reshape(nb, 2)
+    got = oracle.dequantize(oracle.Q4K, raw).reshape(nb, 256)
+    # vectorised over blocks, following the GGML block_q4_K layout description:
+    d = raw[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    dm = raw[:, 2:4].copy().view(np.float16).astype(np.float32)[:, 0]
+    s = raw[:, 4:16].astype(np.uint32)
+    sc = np.zeros((nb, 8), np.uint32)
+    mn = np.zeros((nb, 8), np.uint32)
+    sc[:, :4] = s[:, 0:4] & 63
+    mn[:, :4] = s[:, 4:8] & 63
+    sc[:, 4:] = (s[:, 8:12] & 15) | ((s[:, 0:4] >> 6) << 4)
+    mn[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+    qs = raw[:, 16:].reshape(nb, 4, 32)
+    nib = np.stack([qs & 15, qs >> 4], axis=2).reshape(nb, 8, 32).astype(np.float32)
+    want = (d[:, None, None] * sc[:, :, None].astype(np.float32)) * nib - \
+        (dm[:, None] * mn.astype(np.float32))[:, :, None]
+    assert np.array_equal(got, want.reshape(nb, 256).astype(np.float32))
+
+
+# ---------------------------------------------------------------- hand-built Q6_K blocks
+
+def q6k_block(ql, qh, sc, d):
+    return np.frombuffer(bytes(ql) + bytes(qh) + bytes([s & 0xFF for s in sc]) + f16_bytes(d), np.uint8)
+
+
+def q6_element_position(e):
+    """(ql byte, ql shift, qh byte, qh shift) holding element e of a Q6_K block."""
+    n, r = divmod(e, 128)
+    i, l = divmod(r, 32)
+    ql = 64 * n + l + (32 if i in (1, 3) else 0)
+    return ql, (4 if i >= 2 else 0), 32 * n + l, 2 * i
+
+
+def test_q6k_zero_point_and_sign_of_scales(oracle):
+    # q6 = 32 everywhere: low nibble 0, high bits 2 -> every element decodes to 0
+    ql = [0] * 128
+    qh = [0b10101010] * 64
+    w = oracle.dequantize(oracle.Q6K, q6k_block(ql, qh, [1] * 16, 1.0))
+    assert np.array_equal(w, np.zeros(256, np.float32))
+    # one element at a time with distinct scales: w = d * sc[e // 16] * (q6 - 32)
+    scales = [(-1) ** g * (g + 1) for g in range(16)]
+    for e in [0, 15, 16, 33, 70, 95, 127, 128, 161, 200, 255]:
+        ql = [0] * 128
+        qh = [0b10101010] * 64
+        b, sh, hb, hsh = q6_element_position(e)
+        q6 = 45  # low nibble 13, high bits 2
+        ql[b] |= (q6 & 15) << sh
+        qh[hb] = (qh[hb] & ~(3 << hsh)) | ((q6 >> 4) << hsh)
+        w = oracle.dequantize(oracle.Q6K, q6k_block(ql, qh, scales, 0.5))
+        want = np.zeros(256, np.float32)
+        want[e] = 0.5 * scales[e // 16] * (q6 - 32)
+        assert np.array_equal(w, want), e
+
+
+def test_q5_0_high_bits_follow_qh_bit_order(oracle):
+    for j in range(32):
+        blk = bytearray(22)
+        blk[0:2] = f16_bytes(2.0)
+        blk[2:6] = struct.pack("<I", 1 << j)
+        w = oracle.dequantize(oracle.Q5_0, np.frombuffer(bytes(blk), np.uint8))
+        want = np.full(32, -32.0, np.float32)
+        want[j] = 0.0  # (16 - 16) * 2
+        assert np.array_equal(w, want), j
+
+
+# ---------------------------------------------------------------- packing invariant
+
+@pytest.mark.parametrize("tid", [8, 14, 6, 12])
+def test_pack_keeps_values(oracle, tid):
+    rng = np.random.default_rng(tid)
+    e, b = oracle.type_block(tid)
+    nb = 12
+    raw = rng.integers(0, 256, size=(nb, b), dtype=np.uint8)
+    # keep the f16 scales finite
+    off = {8: 0, 6: 0, 12: 0, 14: 208}[tid]
+    raw[:, off:off + 2] = np.frombuffer(np.float16(0.75).tobytes(), np.uint8)
+    if tid == 12:
+        raw[:, 2:4] = np.frombuffer(np.float16(0.125).tobytes(), np.uint8)
+    q, h, s, d = oracle.pack(tid, raw)
+    wq, wh, ws, wd = oracle.packed_words(tid)
+    assert (len(q), len(h), len(s), len(d)) == (nb * wq, nb * wh, nb * ws, nb * wd)
+    qb = q.view(np.uint8).reshape(nb, -1)
+    if tid == 12:
+        assert np.array_equal(qb, raw)
+    elif tid == 14:
+        assert np.array_equal(qb, raw[:, :128])
+        assert np.array_equal(h.view(np.uint8).reshape(nb, -1), raw[:, 128:192])
+        assert np.array_equal(s.view(np.uint8).reshape(nb, -1), raw[:, 192:208])
+        assert np.all(d == 0.75)
+    elif tid == 8:
+        assert np.array_equal(qb, raw[:, 2:])
+        assert np.all(d == 0.75)
+    else:
+        assert np.array_equal(qb, raw[:, 6:])
+        assert np.array_equal(h.view(np.uint8).reshape(nb, -1), raw[:, 2:6])
+
+
+# ---------------------------------------------------------------- f64 matmul
+
+def test_matmul_f64_matches_numpy_and_a_hand_example(oracle):
+    x = np.array([[1.0, 2.0, 3.0]], np.float32)
+    w = np.array([[1.0, 0.0, -1.0], [0.5, 0.25, 0.125]], np.float32)
+    assert np.array_equal(oracle.matmul_f64(x, w), np.array([[-2.0, 1.375]]))
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((5, 300)).astype(np.float32)
+    w = rng.standard_normal((70, 300)).astype(np.float32)
+    want = x.astype(np.float64) @ w.astype(np.float64).T
+    assert np.allclose(oracle.matmul_f64(x, w), want, rtol=1e-12, atol=1e-12)
+
+
+def test_cpu_baseline_agrees_with_the_f64_oracle(oracle):
+    rng = np.random.default_rng(9)
+    n, k, m = 64, 512, 3
+    raw = oracle.Rng(11).recipe_q8_0(n * k // 32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = oracle.dequantize(oracle.Q8_0, raw).reshape(n, k)
+    want = oracle.matmul_f64(x, w)
+    for threads in (1, 0):
+        got = oracle.cpu_dequant_matmul(oracle.Q8_0, raw, n, k, x, threads=threads)
+        assert oracle.normalized_error(got, want) < 1e-5
+
+
+# ---------------------------------------------------------------- fixture generator
+
+def test_xorshift_fixture_generator(oracle):
+    # gpu/tests.rs:11-23, restated with Python integers
+    s = 11
+    r = oracle.Rng(11)
+    for _ in range(1000):
+        s ^= (s << 13) & 0xFFFFFFFFFFFFFFFF
+        s ^= s >> 7
+        s ^= (s << 17) & 0xFFFFFFFFFFFFFFFF
+        want = np.float32(np.float32(s >> 40) / np.float32(1 << 24) * np.float32(2.0) - np.float32(1.0))
+        assert r.next() == want
