@@ -1,0 +1,252 @@
+"""Benchmark of the gfx950 quantized GGML products on one MI355X.
+
+Step = one Q4_K decode GEMV at M = 1, 4 and 8 (K = 3840, N = 15360, bf16 activations, f32
+out), each on a different copy of the weights: the copies rotate through more than 512 MiB so the
+256 MiB last-level cache cannot serve them. `value` is the weight bytes of the timed steps over
+their wall time (HIP graph replay, inputs resident in HBM). The Q4_K prefill GEMM (M = 512, 1%
+outlier columns) is timed the same way and reported under "gemm".
+
+Roofline entries use the kernels' own durations: each launch is bracketed by events on its own
+stream while the stream is held behind a spin kernel, so the host never starves the queue.
+
+CPU baseline: the oracle's port of the reference CPU path (quant.rs decode + f32-accumulate
+matmul, OpenMP) on the same Q4_K matrix at M = 1, timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "jevons-rs_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16/bf16 MFMA
+ROTATION_BYTES = 512 << 20
+
+METRIC = "Q4_K GEMV weight GB/s (% HBM peak); Q4_K GEMM TFLOPS (% MFMA peak)"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def kernel_times_ms(fn_list, reps):
+    """Average GPU duration of each callable's launch, measured with events that bracket one
+    launch each while the stream is held behind a spin kernel."""
+    import torch
+
+    starts = [[torch.cuda.Event(enable_timing=True) for _ in range(reps)] for _ in fn_list]
+    ends = [[torch.cuda.Event(enable_timing=True) for _ in range(reps)] for _ in fn_list]
+    torch.cuda.synchronize()
+    torch.cuda._sleep(50_000_000)  # holds the stream while the host queues the launches
+    for r in range(reps):
+        for j, fn in enumerate(fn_list):
+            starts[j][r].record()
+            fn(r)
+            ends[j][r].record()
+    torch.cuda.synchronize()
+    return [sum(s.elapsed_time(e) for s, e in zip(starts[j], ends[j])) / reps for j in range(len(fn_list))]
+
+
+def graph_of(fn, count):
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(count):
+                fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    return g
+
+
+def cpu_baseline(raw, n, k, x32):
+    import oracle as O
+
+    threads = O.omp_max_threads()
+    import numpy as np
+
+    wdec = np.empty(n * k, np.float32)
+    nbytes = n * k // 256 * 144
+    O.cpu_dequant_matmul(O.Q4K, raw, n, k, x32[:1], threads=threads, wdec=wdec)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 10.0:
+        O.cpu_dequant_matmul(O.Q4K, raw, n, k, x32[:1], threads=threads, wdec=wdec)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    # single thread on a 1024-row slice of the same matrix
+    rows1 = 1024
+    raw1 = raw[: rows1 * k // 256 * 144]
+    t1 = time.perf_counter()
+    reps1 = 0
+    while time.perf_counter() - t1 < 3.0:
+        O.cpu_dequant_matmul(O.Q4K, raw1, rows1, k, x32[:1], threads=1, wdec=wdec)
+        reps1 += 1
+    dt1 = (time.perf_counter() - t1) / reps1
+    return {
+        "value": round(nbytes / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"Q4_K decode + f32 matmul, M=1, K={k}, N={n} (full matrix), {reps} reps in ~10 s; "
+                  f"1 thread on 1024 rows: {round(rows1 * k // 256 * 144 / dt1 / 1e9, 3)} GB/s",
+        "cpu_model": _cpu_model(),
+    }
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--gemm-steps", type=int, default=50)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import jevons_qmm as jq
+    from jevons_qmm import synth
+
+    n, k = 15360, 3840
+    ms = (1, 4, 8)
+    gpu = jq.Gpu(0)
+    log("device", gpu.info.arch.decode(), "CUs", gpu.info.compute_units)
+    raw = synth.weights(jq.Q4K, 2, n, k)
+    wbytes = raw.size
+    raw_dev = torch.from_numpy(raw).cuda()
+    copies = max(2, math.ceil(ROTATION_BYTES / wbytes))
+    mats = [jq.QMatrix.upload_device(gpu, jq.Q4K, n, k, 1, raw_dev) for _ in range(copies)]
+    del raw_dev
+    log(f"weights {wbytes} B x {copies} copies = {wbytes * copies / 2**20:.0f} MiB")
+
+    x8 = synth.normal_rows(21, 8, k)
+    xb = torch.from_numpy(synth.to_bf16(x8).view(np.int16).copy()).view(torch.bfloat16).cuda()
+    xs = {m: xb[:m].contiguous() for m in ms}
+    outs = {m: torch.empty((m, n), dtype=torch.float32, device="cuda") for m in ms}
+
+    def gemv_step(i):
+        for j, m in enumerate(ms):
+            jq.matmul(gpu, xs[m], m, mats[(3 * i + j) % copies], outs[m])
+
+    gemv_step(0)
+    torch.cuda.synchronize()
+    g_warm = graph_of(gemv_step, args.warmup)
+    g_timed = graph_of(gemv_step, args.steps)
+    g_warm.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g_timed.replay()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    value = 3 * wbytes / (ms_per_step * 1e-3) / 1e9
+
+    # per-kernel durations (M = 1, 4, 8)
+    reps = 100
+    kt = kernel_times_ms([lambda r, m=m: jq.matmul(gpu, xs[m], m, mats[r % copies], outs[m]) for m in ms], reps)
+    per_m = {m: {"kernel_us": round(t * 1e3, 3), "weight_GBps": round(wbytes / (t * 1e-3) / 1e9, 1)}
+             for m, t in zip(ms, kt)}
+    avg_kernel_ms = sum(kt) / len(kt)
+    achieved = wbytes / (avg_kernel_ms * 1e-3) / 1e9
+    log("gemv per M:", per_m)
+
+    # prefill GEMM, M = 512
+    mg = 512
+    xg32 = synth.normal_rows(31, mg, k, outlier_frac=0.01)
+    xg = torch.from_numpy(synth.to_bf16(xg32).view(np.int16).copy()).view(torch.bfloat16).cuda()
+    og = torch.empty((mg, n), dtype=torch.float32, device="cuda")
+    plan = jq.Plan.auto(mats[0], mg, row_invariant=True)
+
+    def gemm_step(i):
+        jq.matmul_plan(gpu, xg, mg, mats[i % copies], og, None, plan)
+
+    gemm_step(0)
+    torch.cuda.synchronize()
+    gg = graph_of(gemm_step, args.gemm_steps)
+    gg.replay()
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    gg.replay()
+    torch.cuda.synchronize()
+    t3 = time.perf_counter()
+    gemm_ms = (t3 - t2) * 1e3 / args.gemm_steps
+    flops = 2.0 * mg * n * k
+    gk = kernel_times_ms([lambda r: gemm_step(r)], 30)[0]
+    gemm = {
+        "workload": f"Q4_K prefill GEMM M={mg} K={k} N={n}, bf16 activations (1% outlier columns x20), f32 out",
+        "plan": {"bm": plan.bm, "bn": plan.bn, "splits": plan.splits},
+        "ms_per_step": round(gemm_ms, 4),
+        "value": round(flops / (gemm_ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "roofline": {"bound": "mfma", "achieved": round(flops / (gk * 1e-3) / 1e12, 2),
+                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(flops / (gk * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+    }
+    log("gemm:", gemm)
+
+    cpu = None if args.no_cpu else cpu_baseline(raw, n, k, x8)
+    if cpu:
+        log("cpu:", cpu)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"Q4_K decode GEMV K={k} N={n}, M in {{1,4,8}} per step, bf16 activations, f32 out",
+            "weight_bytes_per_launch": wbytes,
+            "rotation_copies": copies,
+            "per_m": per_m,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "gemm": gemm,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,174 @@
+/*
+ * jevons_qmm.h — C ABI of the MI355X (gfx950) quantized GGML matrix products.
+ *
+ * Drop-in boundary for jevons-rs's quantized matmul path. Each entry point names the reference
+ * interface it replaces (paths relative to the reference repository root):
+ *   crates/jevons-kernels/src/gemm.rs        QMatrix, Plan, SplitScratch, matmul*, matvec
+ *   crates/jevons-kernels/src/lib.rs         Gpu (device client), Buf (device buffer + length)
+ *   crates/jevons-formats/src/gguf.rs        TensorType ids and block sizes
+ *   crates/jevons-burn/src/kernels.rs        GemmOps::f16_matmul (Burn operator)
+ *   crates/jevons-core/src/model.rs          greedy (argmax of a logit row)
+ *
+ * Conventions
+ *  - Every call returns a jv_status; JV_OK is 0. On failure jv_last_error() returns a message
+ *    for the calling thread that names the type and shape like the reference's Err strings.
+ *    Nothing aborts; bad shapes and short buffers are rejected on the host (the reference's
+ *    launch asserts and CubeCL checked launches, gemm.rs:1137, :1172, :1218, :1285).
+ *  - Buffers passed to products are device pointers with a logical length in elements (the
+ *    reference's Buf length, lib.rs:76-124). Products are asynchronous on `stream`
+ *    (a hipStream_t; NULL is the default stream). jv_sync waits for the device.
+ *  - A jv_ctx is used from one host thread at a time (the reference's API is not Sync).
+ *  - Outputs are out[r, c] = sum_k x[r, k] * W[c, k] accumulated in fp32.
+ */
+#ifndef JEVONS_QMM_H
+#define JEVONS_QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    JV_OK = 0,
+    JV_ERR_INVALID = 1,     /* bad argument, shape or length */
+    JV_ERR_UNSUPPORTED = 2, /* tensor type or encoding without a GPU layout */
+    JV_ERR_HIP = 3,         /* the HIP runtime reported an error */
+    JV_ERR_NO_KERNELS = 4,  /* the gfx950 code object could not be loaded */
+    JV_ERR_NO_MEMORY = 5    /* device allocation failed */
+} jv_status;
+
+/* Kernel weight encodings; values equal FMT_* (gemm.rs:25-30). */
+typedef enum { JV_FMT_Q4K = 0, JV_FMT_Q6K = 1, JV_FMT_Q5_0 = 2, JV_FMT_Q8_0 = 3, JV_FMT_F16 = 4 } jv_fmt;
+
+/* GGML tensor type ids (TensorType::from_id, gguf.rs:120-131). */
+enum {
+    JV_GGML_F32 = 0, JV_GGML_F16 = 1, JV_GGML_Q5_0 = 6, JV_GGML_Q8_0 = 8, JV_GGML_Q4K = 12,
+    JV_GGML_Q6K = 14
+};
+
+/* Activation element type. The reference takes FP16 rows (gemm.rs:405, :537); BF16 and F32
+ * rows are converted to FP16 while they are staged on chip (exact for BF16 magnitudes in
+ * [2^-14, 65504]; F32 rounds to nearest even, as the reference's upload_f16 does). */
+typedef enum { JV_ACT_F16 = 0, JV_ACT_BF16 = 1, JV_ACT_F32 = 2 } jv_act;
+
+/* Output element type. The reference writes FP32; BF16 rounds the FP32 sum to nearest even. */
+typedef enum { JV_OUT_F32 = 0, JV_OUT_BF16 = 1 } jv_out;
+
+/* Launch plan (Plan, gemm.rs:973-979): bm == 0 selects the small-row product (m <= 16).
+ * bm in {32, 64, 128} rows, bn in {64, 128} columns as the reference allows, plus bn = 256
+ * on gfx950; splits in 1..=16 divides K (partials summed in a fixed order). */
+typedef struct {
+    uint32_t bm, bn, splits;
+} jv_plan;
+
+typedef struct jv_ctx jv_ctx;         /* Gpu (lib.rs:17-306) */
+typedef struct jv_qmatrix jv_qmatrix; /* QMatrix (gemm.rs:817-829) */
+typedef struct jv_scratch jv_scratch; /* SplitScratch (gemm.rs:1041-1065) */
+
+typedef struct {
+    int device;
+    int compute_units;
+    int wave_size;
+    size_t lds_bytes;       /* LDS per workgroup */
+    size_t total_memory;
+    char arch[64];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+} jv_device_info;
+
+/* (elements, bytes) per block of a GGML type id; JV_ERR_UNSUPPORTED for other ids
+ * (TensorType::block, gguf.rs:134-144). */
+jv_status jv_type_block(uint32_t ggml_type, uint32_t *elems, uint32_t *bytes);
+
+/* Opens HIP device `device` and loads the gfx950 code object (Gpu::new, lib.rs:181-197).
+ * The code object is looked up in $JV_CODE_OBJECT, else next to this library. */
+jv_status jv_open(int device, jv_ctx **out);
+void jv_close(jv_ctx *ctx);
+jv_status jv_device_info_get(jv_ctx *ctx, jv_device_info *info);
+/* Waits for all queued work on the context's device (Gpu::sync, lib.rs:294-302). */
+jv_status jv_sync(jv_ctx *ctx);
+
+/* Uploads GGML blocks of `ggml_type` for weights [experts * n, k] (QMatrix::upload,
+ * gemm.rs:822-841). `raw` is host memory of exactly experts*n*k/block*size bytes. The blocks
+ * are repacked on the device into the gfx950 layout; decoded values are unchanged. */
+jv_status jv_qmatrix_upload(jv_ctx *ctx, uint32_t ggml_type, size_t n, size_t k, size_t experts,
+                            const void *raw, size_t bytes, jv_qmatrix **out);
+/* Same, with `raw_dev` already in device memory (no host copy). */
+jv_status jv_qmatrix_upload_device(jv_ctx *ctx, uint32_t ggml_type, size_t n, size_t k,
+                                   size_t experts, const void *raw_dev, size_t bytes,
+                                   jv_qmatrix **out);
+/* Uploads the reference's packed regions (QMatrix::from_packed, gemm.rs:844-899; region
+ * sizes per quant::packed_words, quant.rs:127-135). Packed scales must be FP16 values. */
+jv_status jv_qmatrix_from_packed(jv_ctx *ctx, uint32_t ggml_type, size_t n, size_t k,
+                                 size_t experts, const uint32_t *q, size_t nq, const uint32_t *h,
+                                 size_t nh, const uint32_t *s, size_t ns, const float *d,
+                                 size_t nd, jv_qmatrix **out);
+/* Views caller-owned row-major FP16 device weights [n, k] stored as n*k/2 words without a copy
+ * (QMatrix::f16_view / from_f16_words, gemm.rs:903-948). The caller keeps the buffer alive. */
+jv_status jv_qmatrix_f16_view(jv_ctx *ctx, size_t n, size_t k, const void *dev_words,
+                              size_t words, jv_qmatrix **out);
+void jv_qmatrix_free(jv_qmatrix *w);
+/* Device bytes held by the matrix (QMatrix::bytes, gemm.rs:950-952). */
+size_t jv_qmatrix_bytes(const jv_qmatrix *w);
+jv_status jv_qmatrix_shape(const jv_qmatrix *w, uint32_t *fmt, size_t *n, size_t *k,
+                           size_t *experts);
+
+/* Plan::heuristic (gemm.rs:987-1004), unchanged: row-invariant plans never split K or use the
+ * small-row kernel; `groups_target` is the workgroup count that fills the device. */
+jv_plan jv_plan_heuristic(const jv_qmatrix *w, size_t m, int row_invariant, size_t groups_target);
+/* The plan this library picks for gfx950 (256 compute units) when none is given. */
+jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant);
+/* Plan::valid_for (gemm.rs:1006-1015), plus bn = 256. Returns 1 if valid, 0 if not. */
+int jv_plan_valid(const jv_qmatrix *w, size_t m, jv_plan plan);
+
+/* Grow-on-demand split-K partial buffer (SplitScratch, gemm.rs:1041-1065). */
+jv_status jv_scratch_new(jv_ctx *ctx, jv_scratch **out);
+void jv_scratch_free(jv_scratch *s);
+
+/* out[m, n] = x[m, k] . W^T with this library's plan (matmul, gemm.rs:1069-1088). */
+jv_status jv_matmul(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                    const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
+                    jv_scratch *scratch, void *stream);
+/* Product with an explicit plan (matmul_plan, gemm.rs:1093-1119). Plans with splits == 1 are
+ * row invariant: every output row is accumulated in the same order whatever m or the tile. */
+jv_status jv_matmul_plan(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                         const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
+                         jv_scratch *scratch, jv_plan plan, void *stream);
+/* Small-row product, m <= 16 (matvec, gemm.rs:1136-1168). */
+jv_status jv_matvec(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                    const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
+                    void *stream);
+/* Tiled product with split-K (matmul_split, gemm.rs:1206-1257; matmul_tiled :1122-1133 is
+ * splits = 1). `scratch` may be NULL when splits == 1. */
+jv_status jv_matmul_split(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                          const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
+                          uint32_t bm, uint32_t bn, uint32_t splits, jv_scratch *scratch,
+                          void *stream);
+
+/* Burn operator GemmOps::f16_matmul (crates/jevons-burn/src/kernels.rs:52-97): dense row-major
+ * FP16 x [m, k] times FP16 weight [n, k]^T into FP32 out [m, n], with the row-invariant plan
+ * rule of kernels.rs:16-31. n and k must be multiples of 64. */
+jv_status jv_f16_matmul(jv_ctx *ctx, const void *x, size_t m, size_t k, const void *weight,
+                        size_t n, float *out, void *stream);
+
+/* Per-row argmax of FP32 logits [rows, n] with greedy's rule (model.rs:207-219): the first
+ * maximum wins; a row holding a non-finite value or n == 0 yields index -1. `index` is a
+ * device buffer of `rows` int32. `scratch` holds the per-chunk partials. */
+jv_status jv_argmax_rows(jv_ctx *ctx, const float *logits, size_t rows, size_t n,
+                         int32_t *index, jv_scratch *scratch, void *stream);
+
+/* Exactness probes: decode rows [row0, row0 + rows) of `w` with the products' own device
+ * decoder into FP32 (equal to quant::dequantize, quant.rs:83-101) or FP16 (the on-chip weight
+ * tile, round-to-nearest-even of that FP32 value). Outputs are device [rows, k]. */
+jv_status jv_dequant_rows_f32(jv_ctx *ctx, const jv_qmatrix *w, size_t row0, size_t rows,
+                              float *out, void *stream);
+jv_status jv_dequant_rows_f16(jv_ctx *ctx, const jv_qmatrix *w, size_t row0, size_t rows,
+                              uint16_t *out, void *stream);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *jv_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

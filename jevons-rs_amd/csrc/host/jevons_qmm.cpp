@@ -1,0 +1,791 @@
+// Host side of the gfx950 quantized GGML products: device client, weight upload and layout,
+// launch plans, and the C ABI declared in include/jevons_qmm.h.
+//
+// This is the C++ counterpart of crates/jevons-kernels/src/{lib.rs,gemm.rs}: it validates every
+// shape and buffer length on the host (the reference relies on CubeCL's checked launches and
+// launch asserts), loads the kernels from a gfx950 code object with hipModule*, and launches
+// them on the caller's stream.
+
+#include "jevons_qmm.h"
+
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../qmm_params.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+jv_status fail(jv_status st, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return st;
+}
+
+#define JV_HIP(call)                                                                         \
+    do {                                                                                     \
+        hipError_t e_ = (call);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            return fail(e_ == hipErrorOutOfMemory ? JV_ERR_NO_MEMORY : JV_ERR_HIP, "%s: %s", \
+                        #call, hipGetErrorString(e_));                                       \
+    } while (0)
+
+// GGML type table (crates/jevons-formats/src/gguf.rs:120-144).
+bool type_block(uint32_t id, uint32_t *elems, uint32_t *bytes) {
+    switch (id) {
+    case JV_GGML_F32: *elems = 1; *bytes = 4; return true;
+    case JV_GGML_F16: *elems = 1; *bytes = 2; return true;
+    case JV_GGML_Q5_0: *elems = 32; *bytes = 22; return true;
+    case JV_GGML_Q8_0: *elems = 32; *bytes = 34; return true;
+    case JV_GGML_Q4K: *elems = 256; *bytes = 144; return true;
+    case JV_GGML_Q6K: *elems = 256; *bytes = 210; return true;
+    default: return false;
+    }
+}
+
+// The reference's `{kind:?}` spelling of a type id.
+std::string type_name(uint32_t id) {
+    switch (id) {
+    case JV_GGML_F32: return "F32";
+    case JV_GGML_F16: return "F16";
+    case JV_GGML_Q5_0: return "Q5_0";
+    case JV_GGML_Q8_0: return "Q8_0";
+    case JV_GGML_Q4K: return "Q4K";
+    case JV_GGML_Q6K: return "Q6K";
+    default: return "Other(" + std::to_string(id) + ")";
+    }
+}
+
+const char *fmt_kernel_name(jv_fmt f) {
+    switch (f) {
+    case JV_FMT_Q4K: return "q4k";
+    case JV_FMT_Q6K: return "q6k";
+    case JV_FMT_Q5_0: return "q5_0";
+    case JV_FMT_Q8_0: return "q8_0";
+    default: return "f16";
+    }
+}
+
+// K elements per kernel unit of a format (the decoders' KU).
+int fmt_unit(jv_fmt f) { return (f == JV_FMT_Q4K || f == JV_FMT_Q6K) ? 256 : 64; }
+
+std::string library_dir() {
+    Dl_info info;
+    if (dladdr((void *)&jv_open, &info) && info.dli_fname) {
+        std::string p = info.dli_fname;
+        size_t s = p.rfind('/');
+        if (s != std::string::npos) return p.substr(0, s);
+    }
+    return ".";
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// IEEE binary16 <-> binary32 on the host (round to nearest even), for packed-scale checks.
+uint16_t f32_to_f16_bits(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, exp = (x >> 23) & 0xffu, man = x & 0x7fffffu;
+    if (exp == 0xff) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u | (man >> 13) : 0u));
+    const int32_t e = (int32_t)exp - 112;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        const uint32_t full = man | 0x800000u, shift = (uint32_t)(14 - e);
+        uint32_t q = full >> shift;
+        const uint32_t rem = full & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = ((uint32_t)e << 10) | (man >> 13);
+    const uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+    return (uint16_t)(sign | q);
+}
+
+float f16_bits_to_f32(uint16_t b) {
+    const uint32_t sign = (uint32_t)(b & 0x8000u) << 16, exp = (b >> 10) & 0x1fu, man = b & 0x3ffu;
+    uint32_t x;
+    if (exp == 0) {
+        float v = (float)man * (1.0f / 16777216.0f);
+        return sign ? -v : v;
+    }
+    if (exp == 31) x = sign | 0x7f800000u | (man << 13);
+    else x = sign | ((exp + 112u) << 23) | (man << 13);
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+}  // namespace
+
+struct jv_ctx {
+    int device = 0;
+    hipModule_t module = nullptr;
+    std::unordered_map<std::string, hipFunction_t> fns;
+    jv_device_info info{};
+};
+
+struct jv_qmatrix {
+    jv_ctx *ctx = nullptr;
+    uint32_t ggml_type = 0;
+    jv_fmt fmt = JV_FMT_Q4K;
+    size_t n = 0, k = 0, experts = 1;
+    uint8_t *base = nullptr;  // owned allocation holding every region (null for views)
+    const uint8_t *q = nullptr, *h = nullptr, *d = nullptr;
+    size_t bytes = 0;
+};
+
+struct jv_scratch {
+    jv_ctx *ctx = nullptr;
+    void *buf = nullptr;
+    size_t bytes = 0;
+};
+
+namespace {
+
+jv_status get_fn(jv_ctx *ctx, const std::string &name, hipFunction_t *out) {
+    auto it = ctx->fns.find(name);
+    if (it != ctx->fns.end()) {
+        *out = it->second;
+        return JV_OK;
+    }
+    hipFunction_t f = nullptr;
+    hipError_t e = hipModuleGetFunction(&f, ctx->module, name.c_str());
+    if (e != hipSuccess)
+        return fail(JV_ERR_NO_KERNELS, "kernel %s is missing from the code object: %s",
+                    name.c_str(), hipGetErrorString(e));
+    ctx->fns.emplace(name, f);
+    *out = f;
+    return JV_OK;
+}
+
+jv_status launch(jv_ctx *ctx, const std::string &name, dim3 grid, dim3 block, size_t lds,
+                 void *stream, void **args) {
+    hipFunction_t f;
+    jv_status st = get_fn(ctx, name, &f);
+    if (st != JV_OK) return st;
+    JV_HIP(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                                 (unsigned)lds, (hipStream_t)stream, args, nullptr));
+    return JV_OK;
+}
+
+jv_status use_device(jv_ctx *ctx) {
+    if (!ctx) return fail(JV_ERR_INVALID, "null context");
+    JV_HIP(hipSetDevice(ctx->device));
+    return JV_OK;
+}
+
+// Device bytes of each region of the gfx950 layout for `blocks` GGML blocks.
+struct Layout {
+    size_t q = 0, h = 0, d = 0;
+};
+
+Layout layout_for(jv_fmt fmt, size_t blocks) {
+    Layout l;
+    switch (fmt) {
+    case JV_FMT_Q4K: l.q = blocks * 144; break;
+    case JV_FMT_Q6K: l.q = blocks * 208; l.d = blocks * 2; break;
+    case JV_FMT_Q8_0: l.q = blocks * 32; l.d = blocks * 2; break;
+    case JV_FMT_Q5_0: l.q = blocks * 16; l.h = blocks * 4; l.d = blocks * 2; break;
+    default: break;
+    }
+    return l;
+}
+
+// QMatrix::upload / from_packed shape rules (gemm.rs:822-886), up to the weight format.
+jv_status check_upload(uint32_t type, size_t n, size_t k, size_t experts, size_t bytes,
+                       jv_fmt *fmt_out) {
+    uint32_t block, size;
+    if (!type_block(type, &block, &size)) return fail(JV_ERR_UNSUPPORTED, "unsupported type");
+    const std::string kind = type_name(type);
+    if (bytes != experts * n * k / block * size)
+        return fail(JV_ERR_INVALID, "%s [%zux%zu, %zu] has the wrong byte count", kind.c_str(),
+                    experts, n, k);
+    if (bytes % size != 0)
+        return fail(JV_ERR_INVALID, "tensor is not a whole number of blocks");
+    jv_fmt fmt;
+    switch (type) {
+    case JV_GGML_Q4K: fmt = JV_FMT_Q4K; break;
+    case JV_GGML_Q6K: fmt = JV_FMT_Q6K; break;
+    case JV_GGML_Q5_0: fmt = JV_FMT_Q5_0; break;
+    case JV_GGML_Q8_0: fmt = JV_FMT_Q8_0; break;
+    default: return fail(JV_ERR_UNSUPPORTED, "%s has no GPU block layout", kind.c_str());
+    }
+    if (k % 64 != 0 || n % 64 != 0 || k % block != 0)
+        return fail(JV_ERR_INVALID, "%s [%zux%zu, %zu] has an unsupported shape", kind.c_str(),
+                    experts, n, k);
+    if (experts == 0 || n * experts > (size_t)INT32_MAX || k > (size_t)INT32_MAX / 64)
+        return fail(JV_ERR_INVALID, "%s [%zux%zu, %zu] has an unsupported shape", kind.c_str(),
+                    experts, n, k);
+    *fmt_out = fmt;
+    return JV_OK;
+}
+
+// Lays out raw GGML blocks already in device memory (raw_dev) into a new matrix.
+jv_status build_from_device(jv_ctx *ctx, uint32_t type, jv_fmt fmt, size_t n, size_t k,
+                            size_t experts, const void *raw_dev, size_t bytes, jv_qmatrix **out) {
+    uint32_t block, size;
+    type_block(type, &block, &size);
+    const size_t blocks = bytes / size;
+    Layout l = layout_for(fmt, blocks);
+    const size_t oq = 0, oh = align_up(l.q, 256), od = oh + align_up(l.h, 256);
+    const size_t total = std::max<size_t>(od + align_up(l.d, 256), 256);
+    uint8_t *base = nullptr;
+    JV_HIP(hipMalloc((void **)&base, total));
+    auto *w = new jv_qmatrix();
+    w->ctx = ctx;
+    w->ggml_type = type;
+    w->fmt = fmt;
+    w->n = n;
+    w->k = k;
+    w->experts = experts;
+    w->base = base;
+    w->q = base + oq;
+    w->h = base + oh;
+    w->d = base + od;
+    w->bytes = l.q + l.h + l.d;
+    jv_status st = JV_OK;
+    if (fmt == JV_FMT_Q4K) {
+        hipError_t e = hipMemcpy(base + oq, raw_dev, bytes, hipMemcpyDeviceToDevice);
+        if (e != hipSuccess) st = fail(JV_ERR_HIP, "hipMemcpy: %s", hipGetErrorString(e));
+    } else {
+        RepackParams rp{};
+        rp.raw = (const uint8_t *)raw_dev;
+        rp.wq = base + oq;
+        rp.wh = base + oh;
+        rp.wd = base + od;
+        const char *name = nullptr;
+        if (fmt == JV_FMT_Q6K) {
+            rp.chunks = (int64_t)blocks;
+            name = "jv_repack_q6k";
+        } else if (fmt == JV_FMT_Q8_0) {
+            rp.chunks = (int64_t)(blocks / 2);
+            name = "jv_repack_q8_0";
+        } else {
+            rp.chunks = (int64_t)(blocks / 2);
+            name = "jv_repack_q5_0";
+        }
+        void *args[] = {&rp};
+        dim3 grid((unsigned)((rp.chunks + 255) / 256));
+        st = launch(ctx, name, grid, dim3(256), 0, nullptr, args);
+        if (st == JV_OK) {
+            hipError_t e = hipDeviceSynchronize();
+            if (e != hipSuccess) st = fail(JV_ERR_HIP, "repack: %s", hipGetErrorString(e));
+        }
+    }
+    if (st != JV_OK) {
+        hipFree(base);
+        delete w;
+        return st;
+    }
+    *out = w;
+    return JV_OK;
+}
+
+void put_f16(std::vector<uint8_t> &raw, size_t at, float v) {
+    uint16_t b = f32_to_f16_bits(v);
+    raw[at] = (uint8_t)(b & 0xff);
+    raw[at + 1] = (uint8_t)(b >> 8);
+}
+
+// Row tile of a plan -> kernel MT (16-row m-subtiles per workgroup).
+int plan_mt(const jv_plan &p) { return p.bm == 0 ? 1 : (int)p.bm / 16; }
+// Column tile -> NT (16-column n-subtiles per wave; 4 waves).
+int plan_nt(const jv_plan &p) { return p.bm == 0 ? 1 : (int)p.bn / 64; }
+
+bool act_ok(jv_act a) { return a == JV_ACT_F16 || a == JV_ACT_BF16 || a == JV_ACT_F32; }
+bool out_ok(jv_out o) { return o == JV_OUT_F32 || o == JV_OUT_BF16; }
+
+jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                      const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
+                      jv_plan plan, jv_scratch *scratch, void *stream) {
+    jv_status st = use_device(ctx);
+    if (st != JV_OK) return st;
+    if (!w) return fail(JV_ERR_INVALID, "null weight matrix");
+    if (!act_ok(act)) return fail(JV_ERR_INVALID, "unknown activation type %d", (int)act);
+    if (!out_ok(out_type)) return fail(JV_ERR_INVALID, "unknown output type %d", (int)out_type);
+    if (!jv_plan_valid(w, m, plan))
+        return fail(JV_ERR_INVALID, "plan {bm: %u, bn: %u, splits: %u} is not valid for %s [%zu, %zu] at m = %zu",
+                    plan.bm, plan.bn, plan.splits, type_name(w->ggml_type).c_str(), w->n, w->k, m);
+    if (x_len < m * w->k || out_len < m * w->n)
+        return fail(JV_ERR_INVALID, "buffers too short: x holds %zu of %zu elements, out %zu of %zu",
+                    x_len, m * w->k, out_len, m * w->n);
+    if (m == 0) return JV_OK;
+    if (m > (size_t)INT32_MAX) return fail(JV_ERR_INVALID, "m = %zu is too large", m);
+    if (!x || !out) return fail(JV_ERR_INVALID, "null activation or output buffer");
+    if (((uintptr_t)x & 15u) != 0) return fail(JV_ERR_INVALID, "activations must be 16-byte aligned");
+
+    const int MT = plan_mt(plan), NT = plan_nt(plan);
+    const int KU = fmt_unit(w->fmt);
+    const int splits = (int)plan.splits;
+    const int U = (int)(w->k / KU);
+    const int max_units = (U + splits - 1) / splits;
+    const int rows_alloc = (int)std::min<size_t>((size_t)(16 * MT), m);
+    // LDS budget for the staged activation chunk: whole K for small tiles when it fits.
+    const size_t budget = MT == 1 ? 128 * 1024 : 80 * 1024;
+    int kc_units = (int)((budget / (2 * (size_t)rows_alloc) - 8) / (size_t)KU);
+    kc_units = std::max(1, std::min(kc_units, max_units));
+    const int kc = kc_units * KU;
+    const size_t lds = (size_t)rows_alloc * (size_t)(kc + 8) * 2;
+    if (lds > ctx->info.lds_bytes)
+        return fail(JV_ERR_INVALID, "tile needs %zu bytes of LDS, the device has %zu", lds,
+                    ctx->info.lds_bytes);
+
+    QmmParams p{};
+    p.x = x;
+    p.wq = w->q;
+    p.wh = w->h;
+    p.wd = w->d;
+    p.M = (int32_t)m;
+    p.N = (int32_t)w->n;
+    p.K = (int32_t)w->k;
+    p.ldx = (int32_t)w->k;
+    p.ldo = (int32_t)w->n;
+    p.act = (int32_t)act;
+    p.out_type = (int32_t)out_type;
+    p.kc = kc;
+    p.splits = splits;
+    p.split_stride = (int64_t)(m * w->n);
+    if (splits > 1) {
+        if (!scratch) return fail(JV_ERR_INVALID, "split-K plans need a scratch buffer");
+        const size_t need = (size_t)splits * m * w->n * 4;
+        if (scratch->bytes < need) {
+            if (scratch->buf) JV_HIP(hipFree(scratch->buf));
+            scratch->buf = nullptr;
+            scratch->bytes = 0;
+            JV_HIP(hipMalloc(&scratch->buf, need));
+            scratch->bytes = need;
+        }
+        p.out = scratch->buf;
+    } else {
+        p.out = out;
+    }
+    char name[64];
+    snprintf(name, sizeof name, "jv_qmm_%s_m%d_n%d", fmt_kernel_name(w->fmt), MT, NT);
+    dim3 grid((unsigned)(w->n / (size_t)(64 * NT)), (unsigned)((m + 16 * MT - 1) / (16 * MT)),
+              (unsigned)splits);
+    void *args[] = {&p};
+    st = launch(ctx, name, grid, dim3(256), lds, stream, args);
+    if (st != JV_OK || splits == 1) return st;
+    const void *part = scratch->buf;
+    int64_t len = (int64_t)(m * w->n);
+    int sp = splits, ot = (int)out_type;
+    void *rargs[] = {&part, &out, &len, &sp, &ot};
+    return launch(ctx, "jv_reduce_splits", dim3((unsigned)((len + 255) / 256)), dim3(256), 0,
+                  stream, rargs);
+}
+
+jv_status dequant_rows(jv_ctx *ctx, const jv_qmatrix *w, size_t row0, size_t rows, void *out,
+                       int f16_out, void *stream) {
+    jv_status st = use_device(ctx);
+    if (st != JV_OK) return st;
+    if (!w || !out) return fail(JV_ERR_INVALID, "null matrix or output");
+    if (row0 + rows > w->n * w->experts)
+        return fail(JV_ERR_INVALID, "rows [%zu, %zu) are outside the %zu weight rows", row0,
+                    row0 + rows, w->n * w->experts);
+    if (rows == 0) return JV_OK;
+    if (((uintptr_t)out & 15u) != 0) return fail(JV_ERR_INVALID, "output must be 16-byte aligned");
+    DequantParams p{};
+    p.wq = w->q;
+    p.wh = w->h;
+    p.wd = w->d;
+    p.out = out;
+    p.K = (int32_t)w->k;
+    p.row0 = (int32_t)row0;
+    p.rows = (int32_t)rows;
+    p.f16_out = f16_out;
+    std::string name = std::string("jv_dequant_") + fmt_kernel_name(w->fmt);
+    void *args[] = {&p};
+    return launch(ctx, name, dim3((unsigned)((rows + 63) / 64)), dim3(256), 0, stream, args);
+}
+
+}  // namespace
+
+extern "C" {
+
+jv_status jv_type_block(uint32_t ggml_type, uint32_t *elems, uint32_t *bytes) {
+    uint32_t e, b;
+    if (!type_block(ggml_type, &e, &b)) return fail(JV_ERR_UNSUPPORTED, "unsupported tensor type");
+    if (elems) *elems = e;
+    if (bytes) *bytes = b;
+    return JV_OK;
+}
+
+jv_status jv_open(int device, jv_ctx **out) {
+    if (!out) return fail(JV_ERR_INVALID, "null output pointer");
+    *out = nullptr;
+    int count = 0;
+    JV_HIP(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count)
+        return fail(JV_ERR_INVALID, "HIP device %d does not exist (%d devices)", device, count);
+    JV_HIP(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    JV_HIP(hipGetDeviceProperties(&prop, device));
+    if (prop.warpSize != 64 || strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(JV_ERR_UNSUPPORTED,
+                    "the kernels are built for gfx950 (wave64); device %d is %s with %d-lane waves",
+                    device, prop.gcnArchName, prop.warpSize);
+    std::string path;
+    if (const char *env = getenv("JV_CODE_OBJECT")) path = env;
+    else path = library_dir() + "/jevons_qmm.hsaco";
+    hipModule_t mod = nullptr;
+    hipError_t e = hipModuleLoad(&mod, path.c_str());
+    if (e != hipSuccess)
+        return fail(JV_ERR_NO_KERNELS, "cannot load the gfx950 code object %s: %s", path.c_str(),
+                    hipGetErrorString(e));
+    auto *ctx = new jv_ctx();
+    ctx->device = device;
+    ctx->module = mod;
+    ctx->info.device = device;
+    ctx->info.compute_units = prop.multiProcessorCount;
+    ctx->info.wave_size = prop.warpSize;
+    ctx->info.lds_bytes = prop.sharedMemPerBlock;
+    ctx->info.total_memory = prop.totalGlobalMem;
+    snprintf(ctx->info.arch, sizeof ctx->info.arch, "%.63s", prop.gcnArchName);
+    *out = ctx;
+    return JV_OK;
+}
+
+void jv_close(jv_ctx *ctx) {
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    if (ctx->module) hipModuleUnload(ctx->module);
+    delete ctx;
+}
+
+jv_status jv_device_info_get(jv_ctx *ctx, jv_device_info *info) {
+    if (!ctx || !info) return fail(JV_ERR_INVALID, "null argument");
+    *info = ctx->info;
+    return JV_OK;
+}
+
+jv_status jv_sync(jv_ctx *ctx) {
+    jv_status st = use_device(ctx);
+    if (st != JV_OK) return st;
+    JV_HIP(hipDeviceSynchronize());
+    return JV_OK;
+}
+
+jv_status jv_qmatrix_upload(jv_ctx *ctx, uint32_t ggml_type, size_t n, size_t k, size_t experts,
+                            const void *raw, size_t bytes, jv_qmatrix **out) {
+    if (!out) return fail(JV_ERR_INVALID, "null output pointer");
+    *out = nullptr;
+    jv_status st = use_device(ctx);
+    if (st != JV_OK) return st;
+    jv_fmt fmt;
+    if ((st = check_upload(ggml_type, n, k, experts, bytes, &fmt)) != JV_OK) return st;
+    if (!raw) return fail(JV_ERR_INVALID, "null weight bytes");
+    void *tmp = nullptr;
+    JV_HIP(hipMalloc(&tmp, std::max<size_t>(bytes, 16)));
+    hipError_t e = hipMemcpy(tmp, raw, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        hipFree(tmp);
+        return fail(JV_ERR_HIP, "hipMemcpy: %s", hipGetErrorString(e));
+    }
+    st = build_from_device(ctx, ggml_type, fmt, n, k, experts, tmp, bytes, out);
+    hipFree(tmp);
+    return st;
+}
+
+jv_status jv_qmatrix_upload_device(jv_ctx *ctx, uint32_t ggml_type, size_t n, size_t k,
+                                   size_t experts, const void *raw_dev, size_t bytes,
+                                   jv_qmatrix **out) {
+    if (!out) return fail(JV_ERR_INVALID, "null output pointer");
+    *out = nullptr;
+    jv_status st = use_device(ctx);
+    if (st != JV_OK) return st;
+    jv_fmt fmt;
+    if ((st = check_upload(ggml_type, n, k, experts, bytes, &fmt)) != JV_OK) return st;
+    if (!raw_dev) return fail(JV_ERR_INVALID, "null weight bytes");
+    return build_from_device(ctx, ggml_type, fmt, n, k, experts, raw_dev, bytes, out);
+}
+
+jv_status jv_qmatrix_from_packed(jv_ctx *ctx, uint32_t ggml_type, size_t n, size_t k,
+                                 size_t experts, const uint32_t *q, size_t nq, const uint32_t *h,
+                                 size_t nh, const uint32_t *s, size_t ns, const float *d,
+                                 size_t nd, jv_qmatrix **out) {
+    if (!out) return fail(JV_ERR_INVALID, "null output pointer");
+    *out = nullptr;
+    uint32_t block, size;
+    if (!type_block(ggml_type, &block, &size)) return fail(JV_ERR_UNSUPPORTED, "unsupported type");
+    const std::string kind = type_name(ggml_type);
+    size_t wq = 0, wh = 0, ws = 0, wd = 0;  // quant::packed_words (quant.rs:127-135)
+    switch (ggml_type) {
+    case JV_GGML_Q4K: wq = 36; break;
+    case JV_GGML_Q6K: wq = 32; wh = 16; ws = 4; wd = 1; break;
+    case JV_GGML_Q5_0: wq = 4; wh = 1; wd = 1; break;
+    case JV_GGML_Q8_0: wq = 8; wd = 1; break;
+    default: return fail(JV_ERR_UNSUPPORTED, "%s weights are not supported", kind.c_str());
+    }
+    const size_t blocks = experts * n * k / block;
+    if (k % 64 != 0 || n % 64 != 0 || k % block != 0 || nq != blocks * wq || nh != blocks * wh ||
+        ns != blocks * ws || nd != blocks * wd)
+        return fail(JV_ERR_INVALID, "%s [%zux%zu, %zu] has an unsupported shape", kind.c_str(),
+                    experts, n, k);
+    if ((nq && !q) || (nh && !h) || (ns && !s) || (nd && !d))
+        return fail(JV_ERR_INVALID, "null packed region");
+    // Rebuild the GGML blocks (the inverse of quant::pack, quant.rs:156-193).
+    std::vector<uint8_t> raw(blocks * size);
+    for (size_t b = 0; b < blocks; ++b) {
+        uint8_t *o = raw.data() + b * size;
+        if (wd) {
+            float v = d[b];
+            if (f16_bits_to_f32(f32_to_f16_bits(v)) != v && !(std::isnan(v)))
+                return fail(JV_ERR_INVALID, "%s packed scale %zu (%g) is not an FP16 value",
+                            kind.c_str(), b, (double)v);
+        }
+        switch (ggml_type) {
+        case JV_GGML_Q4K: memcpy(o, q + 36 * b, 144); break;
+        case JV_GGML_Q6K:
+            memcpy(o, q + 32 * b, 128);
+            memcpy(o + 128, h + 16 * b, 64);
+            memcpy(o + 192, s + 4 * b, 16);
+            put_f16(raw, b * size + 208, d[b]);
+            break;
+        case JV_GGML_Q5_0:
+            put_f16(raw, b * size, d[b]);
+            memcpy(o + 2, h + b, 4);
+            memcpy(o + 6, q + 4 * b, 16);
+            break;
+        case JV_GGML_Q8_0:
+            put_f16(raw, b * size, d[b]);
+            memcpy(o + 2, q + 8 * b, 32);
+            break;
+        }
+    }
+    return jv_qmatrix_upload(ctx, ggml_type, n, k, experts, raw.data(), raw.size(), out);
+}
+
+jv_status jv_qmatrix_f16_view(jv_ctx *ctx, size_t n, size_t k, const void *dev_words, size_t words,
+                              jv_qmatrix **out) {
+    if (!out) return fail(JV_ERR_INVALID, "null output pointer");
+    *out = nullptr;
+    if (!ctx) return fail(JV_ERR_INVALID, "null context");
+    if (k % 64 != 0 || n % 64 != 0 || words != n * k / 2 || n > (size_t)INT32_MAX)
+        return fail(JV_ERR_INVALID, "F16 [%zu, %zu] has an unsupported shape", n, k);
+    if (!dev_words || ((uintptr_t)dev_words & 15u) != 0)
+        return fail(JV_ERR_INVALID, "F16 weights must be a 16-byte aligned device buffer");
+    auto *w = new jv_qmatrix();
+    w->ctx = ctx;
+    w->ggml_type = JV_GGML_F16;
+    w->fmt = JV_FMT_F16;
+    w->n = n;
+    w->k = k;
+    w->experts = 1;
+    w->q = (const uint8_t *)dev_words;
+    w->h = w->q;
+    w->d = w->q;
+    w->bytes = n * k * 2;
+    *out = w;
+    return JV_OK;
+}
+
+void jv_qmatrix_free(jv_qmatrix *w) {
+    if (!w) return;
+    if (w->base) {
+        hipSetDevice(w->ctx->device);
+        hipFree(w->base);
+    }
+    delete w;
+}
+
+size_t jv_qmatrix_bytes(const jv_qmatrix *w) { return w ? w->bytes : 0; }
+
+jv_status jv_qmatrix_shape(const jv_qmatrix *w, uint32_t *fmt, size_t *n, size_t *k,
+                           size_t *experts) {
+    if (!w) return fail(JV_ERR_INVALID, "null matrix");
+    if (fmt) *fmt = (uint32_t)w->fmt;
+    if (n) *n = w->n;
+    if (k) *k = w->k;
+    if (experts) *experts = w->experts;
+    return JV_OK;
+}
+
+// Plan::heuristic (gemm.rs:987-1004), tile_n (:968-971) and choose_splits (:1032-1038).
+jv_plan jv_plan_heuristic(const jv_qmatrix *w, size_t m, int row_invariant, size_t groups_target) {
+    if (!w) return jv_plan{0, 0, 0};
+    const uint32_t bm = m <= 32 ? 32 : 64;
+    const uint32_t bn = w->n % 128 == 0 ? 128 : 64;
+    if (row_invariant) return jv_plan{bm, bn, 1};
+    if (m <= 2) return jv_plan{0, bn, 1};
+    const size_t base = (w->n / bn) * ((m + bm - 1) / bm);
+    const size_t steps = w->k / 64;
+    uint32_t splits = 1;
+    while (splits < 16 && base * splits < groups_target && steps / (splits * 2) >= 4) splits *= 2;
+    return jv_plan{bm, bn, splits};
+}
+
+// gfx950 choice: the small-row kernel up to 16 rows; otherwise the row tile that covers m with
+// the least padding, then the widest column tile that still gives every compute unit a
+// workgroup, then (outside prefill) split-K until the grid fills the device.
+jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
+    if (!w) return jv_plan{0, 0, 0};
+    if (m <= 16) return jv_plan{0, 64, 1};
+    const uint32_t bm = m <= 32 ? 32 : (m <= 64 ? 64 : 128);
+    const size_t cus = w->ctx ? (size_t)std::max(1, w->ctx->info.compute_units) : 256;
+    const size_t mtiles = (m + bm - 1) / bm;
+    uint32_t bn = 64;
+    for (uint32_t c : {256u, 128u}) {
+        if (w->n % c == 0 && (w->n / c) * mtiles >= cus) {
+            bn = c;
+            break;
+        }
+    }
+    uint32_t splits = 1;
+    if (!row_invariant) {
+        const size_t base = (w->n / bn) * mtiles;
+        const size_t units = w->k / (size_t)fmt_unit(w->fmt);
+        while (splits < 16 && base * splits < cus && units / (splits * 2) >= 4) splits *= 2;
+    }
+    return jv_plan{bm, bn, splits};
+}
+
+// Plan::valid_for (gemm.rs:1006-1015); gfx950 also accepts 256-column tiles.
+int jv_plan_valid(const jv_qmatrix *w, size_t m, jv_plan p) {
+    if (!w) return 0;
+    if (p.bm == 0) return m <= 16 && p.splits == 1;
+    const bool bm_ok = p.bm == 32 || p.bm == 64 || p.bm == 128;
+    const bool bn_ok = p.bn == 64 || p.bn == 128 || p.bn == 256;
+    return bm_ok && bn_ok && w->n % p.bn == 0 && p.splits >= 1 && p.splits <= 16 &&
+           w->k / 64 >= p.splits;
+}
+
+jv_status jv_scratch_new(jv_ctx *ctx, jv_scratch **out) {
+    if (!ctx || !out) return fail(JV_ERR_INVALID, "null argument");
+    auto *s = new jv_scratch();
+    s->ctx = ctx;
+    *out = s;
+    return JV_OK;
+}
+
+void jv_scratch_free(jv_scratch *s) {
+    if (!s) return;
+    if (s->buf) {
+        hipSetDevice(s->ctx->device);
+        hipFree(s->buf);
+    }
+    delete s;
+}
+
+jv_status jv_matmul(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                    const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
+                    jv_scratch *scratch, void *stream) {
+    if (!w) return fail(JV_ERR_INVALID, "null weight matrix");
+    return run_product(ctx, x, act, x_len, m, w, out, out_type, out_len,
+                       jv_plan_auto(w, m, 0), scratch, stream);
+}
+
+jv_status jv_matmul_plan(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                         const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
+                         jv_scratch *scratch, jv_plan plan, void *stream) {
+    return run_product(ctx, x, act, x_len, m, w, out, out_type, out_len, plan, scratch, stream);
+}
+
+jv_status jv_matvec(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                    const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
+                    void *stream) {
+    if (m > 16) return fail(JV_ERR_INVALID, "matvec handles at most 16 rows, got %zu", m);
+    return run_product(ctx, x, act, x_len, m, w, out, out_type, out_len, jv_plan{0, 64, 1},
+                       nullptr, stream);
+}
+
+jv_status jv_matmul_split(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                          const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
+                          uint32_t bm, uint32_t bn, uint32_t splits, jv_scratch *scratch,
+                          void *stream) {
+    if (bm == 0) return fail(JV_ERR_INVALID, "matmul_split needs a row tile (bm > 0)");
+    return run_product(ctx, x, act, x_len, m, w, out, out_type, out_len,
+                       jv_plan{bm, bn, splits}, scratch, stream);
+}
+
+// crates/jevons-burn/src/kernels.rs:52-97 with the row-invariant plan rule of :16-31.
+jv_status jv_f16_matmul(jv_ctx *ctx, const void *x, size_t m, size_t k, const void *weight,
+                        size_t n, float *out, void *stream) {
+    if (!ctx) return fail(JV_ERR_INVALID, "null context");
+    if (k % 64 != 0 || n % 64 != 0)
+        return fail(JV_ERR_INVALID, "f16 matmul weight shape (N and K must be multiples of 64)");
+    jv_qmatrix view;
+    view.ctx = ctx;
+    view.ggml_type = JV_GGML_F16;
+    view.fmt = JV_FMT_F16;
+    view.n = n;
+    view.k = k;
+    view.q = view.h = view.d = (const uint8_t *)weight;
+    if (!weight || ((uintptr_t)weight & 15u) != 0)
+        return fail(JV_ERR_INVALID, "F16 weights must be a 16-byte aligned device buffer");
+    uint32_t bm, bn;
+    if (m <= 32) {
+        if (k > 8192) { bm = 128; bn = 128; }
+        else if (n >= 16384 && n < 65536 && n % 128 == 0) { bm = 64; bn = 128; }
+        else { bm = 32; bn = 64; }
+    } else if (m <= 64) {
+        bm = 64; bn = n % 128 == 0 ? 128 : 64;
+    } else {
+        bm = 128; bn = n % 128 == 0 ? 128 : 64;
+    }
+    return run_product(ctx, x, JV_ACT_F16, m * k, m, &view, out, JV_OUT_F32, m * n,
+                       jv_plan{bm, bn, 1}, nullptr, stream);
+}
+
+jv_status jv_argmax_rows(jv_ctx *ctx, const float *logits, size_t rows, size_t n, int32_t *index,
+                         jv_scratch *scratch, void *stream) {
+    jv_status st = use_device(ctx);
+    if (st != JV_OK) return st;
+    if (rows == 0) return JV_OK;
+    if (!index || (n && !logits)) return fail(JV_ERR_INVALID, "null buffer");
+    if (!scratch) return fail(JV_ERR_INVALID, "argmax needs a scratch buffer");
+    if (n > (size_t)INT32_MAX || rows > 65535)
+        return fail(JV_ERR_INVALID, "argmax of %zu rows x %zu is too large", rows, n);
+    const int chunk = 8192;
+    int chunks = (int)((n + chunk - 1) / chunk);
+    const size_t need = std::max<size_t>(rows * (size_t)chunks * 8, 16);
+    if (scratch->bytes < need) {
+        if (scratch->buf) JV_HIP(hipFree(scratch->buf));
+        scratch->buf = nullptr;
+        scratch->bytes = 0;
+        JV_HIP(hipMalloc(&scratch->buf, need));
+        scratch->bytes = need;
+    }
+    float *pval = (float *)scratch->buf;
+    int *pidx = (int *)((uint8_t *)scratch->buf + rows * (size_t)chunks * 4);
+    if (chunks > 0) {
+        int64_t nn = (int64_t)n;
+        int ch = chunk;
+        void *a1[] = {&logits, &nn, &ch, &pval, &pidx};
+        st = launch(ctx, "jv_argmax_partial", dim3((unsigned)chunks, (unsigned)rows), dim3(256), 0,
+                    stream, a1);
+        if (st != JV_OK) return st;
+    }
+    void *a2[] = {&pval, &pidx, &chunks, &index};
+    return launch(ctx, "jv_argmax_final", dim3((unsigned)rows), dim3(256), 0, stream, a2);
+}
+
+jv_status jv_dequant_rows_f32(jv_ctx *ctx, const jv_qmatrix *w, size_t row0, size_t rows,
+                              float *out, void *stream) {
+    return dequant_rows(ctx, w, row0, rows, out, 0, stream);
+}
+
+jv_status jv_dequant_rows_f16(jv_ctx *ctx, const jv_qmatrix *w, size_t row0, size_t rows,
+                              uint16_t *out, void *stream) {
+    return dequant_rows(ctx, w, row0, rows, out, 1, stream);
+}
+
+const char *jv_last_error(void) { return g_error.c_str(); }
+
+}  // extern "C"

@@ -1,0 +1,44 @@
+// Launch parameters shared by the host library and the gfx950 kernels (passed by value).
+#ifndef JV_QMM_PARAMS_H
+#define JV_QMM_PARAMS_H
+
+#include <stdint.h>
+
+// Product out[m, n] = sum_k x[m, k] * W[n, k]. Weight regions follow the device layout of the
+// weight format (see the format decoders in kernels/qmm.hip).
+struct QmmParams {
+    const void *x;       // activations [M][ldx], element type `act`
+    void *out;           // [M][ldo] of `out_type`, or FP32 split partials when splits > 1
+    const uint8_t *wq;   // quant region
+    const uint8_t *wh;   // high-bit region (Q5_0)
+    const uint8_t *wd;   // FP16 block scales (Q6_K, Q8_0, Q5_0)
+    int32_t M, N, K;     // N = weight rows, K = reduction length
+    int32_t ldx, ldo;    // row strides in elements
+    int32_t act;         // 0 f16, 1 bf16, 2 f32
+    int32_t out_type;    // 0 f32, 1 bf16 (ignored for split partials, which are f32)
+    int32_t kc;          // K staged in LDS per chunk (multiple of the format's K unit)
+    int32_t splits;      // grid z; slice z covers units [z*U/splits, (z+1)*U/splits)
+    int64_t split_stride;  // elements between partial planes
+};
+
+// Decode probe: rows [row0, row0 + rows) of a weight matrix into [rows][K].
+struct DequantParams {
+    const uint8_t *wq;
+    const uint8_t *wh;
+    const uint8_t *wd;
+    void *out;
+    int32_t K;
+    int32_t row0, rows;
+    int32_t f16_out;     // 0: FP32 values, 1: FP16 tile values
+};
+
+// GGML blocks (device copy of the upload) -> device layout.
+struct RepackParams {
+    const uint8_t *raw;
+    uint8_t *wq;
+    uint8_t *wh;
+    uint8_t *wd;
+    int64_t chunks;      // work items (format-specific unit of the repack)
+};
+
+#endif

@@ -1,0 +1,311 @@
+"""GPU parity of the gfx950 products against the CPU oracle (quant.rs decode + f64 matmul).
+
+Bars: dequantized weights bit-exact (FP32 decode == quant::dequantize; FP16 tile == round to
+nearest even of it); outputs within 1e-3 of max|f64 oracle| (the reference's own bar is 2e-3,
+crates/jevons-gemma4-diffusion/src/gpu/tests.rs:427-480); plans without split-K bitwise
+identical to each other (spec R8).
+"""
+import numpy as np
+import pytest
+import torch
+
+import jevons_qmm as jq
+import oracle as O
+from helpers import activations, err, f16_tensor, oracle_product, say
+from jevons_qmm import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+FORMATS = [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0), ("q5_0", jq.Q5_0), ("f16", jq.F16)]
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    g = jq.Gpu(0)
+    say("device", g.info.arch.decode(), "CUs", g.info.compute_units, "LDS", g.info.lds_bytes)
+    yield g
+
+
+def make_matrix(gpu, type_id, n, k, seed, raw=None):
+    if raw is None:
+        raw = synth.weights(type_id, seed, n, k)
+    if type_id == jq.F16:
+        t = torch.from_numpy(raw.view(np.float16).reshape(n, k).copy()).cuda()
+        return jq.QMatrix.f16_view(gpu, n, k, t), raw
+    return jq.QMatrix.upload(gpu, type_id, n, k, 1, raw), raw
+
+
+# ------------------------------------------------------------------ exact weight decode
+
+@pytest.mark.parametrize("name,type_id", FORMATS)
+def test_device_decode_is_bit_exact(gpu, name, type_id):
+    n, k = 128, 1024
+    say("decode", name, n, k)
+    w, raw = make_matrix(gpu, type_id, n, k, seed=3)
+    want = O.dequantize(type_id, raw).reshape(n, k)
+    got = jq.dequant_rows(gpu, w, 0, n).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    tile = jq.dequant_rows(gpu, w, 0, n, f16=True).cpu().numpy()
+    assert np.array_equal(tile.view(np.uint16), want.astype(np.float16).view(np.uint16))
+    # a row range that starts inside the matrix
+    part = jq.dequant_rows(gpu, w, 37, 50).cpu().numpy()
+    assert np.array_equal(part.view(np.uint32), want[37:87].view(np.uint32))
+
+
+def test_decode_of_reference_recipes_is_bit_exact(gpu):
+    # Q8_0 weights of gpu/tests.rs:431-436 and the Q6_K table of :546-554
+    rng = O.Rng(11)
+    for type_id, raw, n, k in [(jq.Q8_0, rng.recipe_q8_0(256 * 512 // 32), 256, 512),
+                               (jq.Q6K, rng.recipe_q6k(64 * 512 // 256), 64, 512)]:
+        w = jq.QMatrix.upload(gpu, type_id, n, k, 1, raw)
+        want = O.dequantize(type_id, raw).reshape(n, k)
+        got = jq.dequant_rows(gpu, w, 0, n).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), type_id
+
+
+def test_from_packed_equals_upload(gpu):
+    for type_id in (jq.Q4K, jq.Q6K, jq.Q8_0, jq.Q5_0):
+        n, k = 64, 512
+        raw = synth.weights(type_id, 5, n, k)
+        q, h, s, d = O.pack(type_id, raw)
+        w = jq.QMatrix.from_packed(gpu, type_id, n, k, 1, q, h, s, d)
+        got = jq.dequant_rows(gpu, w, 0, n).cpu().numpy()
+        assert np.array_equal(got, O.dequantize(type_id, raw).reshape(n, k)), type_id
+
+
+# ------------------------------------------------------------------ every plan, small shapes
+
+def all_plans(w, m):
+    plans = [jq.Plan(0, 64, 1)]
+    for bm in jq.Plan.ROW_TILES:
+        for bn in jq.Plan.GFX950_COL_TILES:
+            for splits in (1, 2, 8):
+                plans.append(jq.Plan(bm, bn, splits))
+    return [p for p in plans if p.valid_for(w, m)]
+
+
+@pytest.mark.parametrize("name,type_id", FORMATS)
+@pytest.mark.parametrize("act", ["bf16", "f16", "f32"])
+def test_every_plan_matches_oracle_and_tiles_are_row_invariant(gpu, name, type_id, act):
+    n, k = 256, 512
+    w, raw = make_matrix(gpu, type_id, n, k, seed=7)
+    scratch = jq.SplitScratch(gpu)
+    for m in (1, 3, 16, 70, 150):
+        x32 = synth.normal_rows(100 + m, m, k)
+        x, xv = activations(act, x32)
+        if act == "f32":
+            xv = xv.astype(np.float16).astype(np.float32)  # the kernels stage FP16 activations
+        want = oracle_product(type_id, raw, n, k, xv)
+        reference = None
+        for plan in all_plans(w, m):
+            say(name, act, "m", m, plan)
+            out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+            jq.matmul_plan(gpu, x, m, w, out, scratch, plan)
+            got = out.cpu().numpy()
+            e = err(got, want)
+            assert e <= TOL, f"m={m} {plan}: normalized error {e:.2e}"
+            if plan.splits == 1:
+                if reference is None:
+                    reference = got
+                else:
+                    assert np.array_equal(reference, got), f"m={m} {plan} is not row invariant"
+
+
+def test_reference_dense_plan_recipe(gpu):
+    """every_tunable_dense_plan_matches_reference_and_tiles_are_row_invariant
+    (gpu/tests.rs:427-480): Q8_0 N=256 K=512, FP16 rows, every reference plan."""
+    n, k = 256, 512
+    rng = O.Rng(11)
+    raw = rng.recipe_q8_0(n * k // 32)
+    w = jq.QMatrix.upload(gpu, jq.Q8_0, n, k, 1, raw)
+    dense = O.dequantize(jq.Q8_0, raw).reshape(n, k)
+    scratch = jq.SplitScratch(gpu)
+    for m in (3, 16, 70, 150):
+        xh = rng.h16_vec(m * k, 1.0).reshape(m, k)
+        x = torch.from_numpy(xh.astype(np.float16)).cuda()
+        want = O.matmul_f64(xh, dense)
+        plans = [jq.Plan(0, 128, 1)] + [jq.Plan(bm, bn, s) for bm in jq.Plan.ROW_TILES
+                                        for bn in jq.Plan.COL_TILES for s in (1, 2, 8)]
+        reference = None
+        for plan in [p for p in plans if p.valid_for(w, m)]:
+            out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+            jq.matmul_plan(gpu, x, m, w, out, scratch, plan)
+            got = out.cpu().numpy()
+            assert err(got, want) <= 2e-3 and err(got, want) <= TOL, (m, plan)
+            if plan.bm > 0 and plan.splits == 1:
+                if reference is None:
+                    reference = got
+                else:
+                    assert np.array_equal(reference, got), (m, plan)
+
+
+def test_bf16_output_rounds_the_f32_result(gpu):
+    n, k, m = 256, 512, 20
+    w, raw = make_matrix(gpu, jq.Q4K, n, k, seed=9)
+    x, _ = activations("bf16", synth.normal_rows(1, m, k))
+    o32 = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    o16 = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    plan = jq.Plan(32, 128, 1)
+    jq.matmul_plan(gpu, x, m, w, o32, None, plan)
+    jq.matmul_plan(gpu, x, m, w, o16, None, plan)
+    assert torch.equal(o32.to(torch.bfloat16), o16)
+
+
+# ------------------------------------------------------------------ workload shapes
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_q4k_decode_gemv_full_shape(gpu, m):
+    """Q4_K GEMV at K=3840, N=15360 (every output checked against the f64 oracle)."""
+    n, k = 15360, 3840
+    say("q4k gemv", m, n, k)
+    w, raw = make_matrix(gpu, jq.Q4K, n, k, seed=2)
+    x32 = synth.normal_rows(20 + m, m, k)
+    x, xv = activations("bf16", x32)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    jq.matmul(gpu, x, m, w, out)
+    got = out.cpu().numpy()
+    want = oracle_product(jq.Q4K, raw, n, k, xv)
+    e = err(got, want)
+    say("normalized error", e)
+    assert e <= TOL
+
+
+def test_q4k_prefill_gemm_m512_rows(gpu):
+    """Q4_K GEMM M=512, K=3840, N=15360 with 1% outlier columns: 48 sampled rows against the
+    f64 oracle, and every row bitwise equal to the row-invariant small-row plan's."""
+    m, n, k = 512, 15360, 3840
+    say("q4k gemm", m, n, k)
+    w, raw = make_matrix(gpu, jq.Q4K, n, k, seed=2)
+    x32 = synth.normal_rows(31, m, k, outlier_frac=0.01)
+    x, xv = activations("bf16", x32)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    plan = jq.Plan.auto(w, m, row_invariant=True)
+    jq.matmul_plan(gpu, x, m, w, out, None, plan)
+    got = out.cpu().numpy()
+    rows = np.random.default_rng(0).choice(m, 48, replace=False)
+    want = oracle_product(jq.Q4K, raw, n, k, xv[rows])
+    e = err(got[rows], want)
+    say("plan", plan, "normalized error", e)
+    assert e <= TOL
+    for r0 in (0, 200, 496):
+        o1 = torch.empty((16, n), dtype=torch.float32, device="cuda")
+        jq.matmul_plan(gpu, x[r0:r0 + 16].contiguous(), 16, w, o1, None, jq.Plan(0, 64, 1))
+        assert torch.equal(o1, out[r0:r0 + 16]), r0
+
+
+# ------------------------------------------------------------------ lm_head argmax
+
+def test_argmax_follows_greedy(gpu):
+    s = jq.SplitScratch(gpu)
+    rows = [
+        [1000.0, 1000.0 + float(np.log(np.float32(2.0))), 0.0],  # model.rs:225-233
+        [3.0, 3.0, 1.0],
+        [float("inf"), 0.0, 0.0],
+        [1.0, float("nan"), 2.0],
+        [-1.0, -0.5, -0.5],
+    ]
+    t = torch.tensor(rows, dtype=torch.float32, device="cuda")
+    got = jq.argmax_rows(gpu, t, s).cpu().tolist()
+    assert got == [1, 0, -1, -1, 1]
+    # ties across chunk boundaries: the first maximum wins
+    big = torch.zeros((2, 70000), dtype=torch.float32, device="cuda")
+    big[0, 9000] = 5.0
+    big[0, 60000] = 5.0
+    big[1, 69999] = 1.0
+    assert jq.argmax_rows(gpu, big, s).cpu().tolist() == [9000, 69999]
+    empty = torch.zeros((3, 0), dtype=torch.float32, device="cuda")
+    assert jq.argmax_rows(gpu, empty, s).cpu().tolist() == [-1, -1, -1]
+
+
+@pytest.mark.parametrize("m", [1, 8, 32])
+def test_q6k_lm_head_logits_and_argmax(gpu, m):
+    """Q6_K vocabulary projection K=3840 on 16384 rows of the vocabulary: logits against the f64
+    oracle, argmax equal to the oracle's greedy on the oracle logits wherever the oracle's top-2
+    gap exceeds the error bound."""
+    n, k = 16384, 3840
+    w, raw = make_matrix(gpu, jq.Q6K, n, k, seed=4)
+    x, xv = activations("bf16", synth.normal_rows(50 + m, m, k))
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    jq.matmul(gpu, x, m, w, out, jq.SplitScratch(gpu))
+    want = oracle_product(jq.Q6K, raw, n, k, xv)
+    e = err(out.cpu().numpy(), want)
+    assert e <= TOL
+    idx = jq.argmax_rows(gpu, out, jq.SplitScratch(gpu)).cpu().numpy()
+    bound = 2 * e * np.abs(want).max()
+    for r in range(m):
+        srt = np.sort(want[r])
+        oracle_idx, _ = O.greedy(want[r].astype(np.float32))
+        if srt[-1] - srt[-2] > bound:
+            assert idx[r] == int(np.argmax(want[r])), r
+        assert idx[r] == O.greedy(out[r].cpu().numpy())[0]
+
+
+# ------------------------------------------------------------------ Burn operator
+
+@pytest.mark.parametrize("m,n,k", [(32, 64, 256), (32, 4160, 512), (64, 256, 1024), (512, 384, 512),
+                                   (32, 6144, 4096), (128, 4096, 4096), (32, 28672, 4096)])
+def test_f16_matmul_matches_f32_matmul(gpu, m, n, k):
+    """f16_matmul_matches_burn_matmul_for_canvas_and_prefill_rows
+    (crates/jevons-burn/src/kernels.rs:136-185), tolerance 2e-3 * max(scale, 1)."""
+    g = torch.Generator().manual_seed(m * 7 + n)
+    x = (torch.rand((m, k), generator=g) * 2 - 1).half()
+    wt = ((torch.rand((n, k), generator=g) * 2 - 1) * 0.1).half()
+    want = (x.float() @ wt.float().T)
+    got = jq.f16_matmul(gpu, x.cuda(), wt.cuda()).cpu()
+    worst = (want - got).abs().max().item()
+    scale = want.abs().max().item()
+    assert worst <= 2e-3 * max(scale, 1.0), worst
+
+
+def test_f16_matmul_outputs_beyond_the_fp16_range(gpu):
+    """kernels.rs:187-218: outputs ~ 1.2e5 come out in full."""
+    g = torch.Generator().manual_seed(1)
+    x = (29 + 2 * torch.rand((128, 4096), generator=g)).half()
+    wt = (0.9 + 0.2 * torch.rand((256, 4096), generator=g)).half()
+    want = x.float() @ wt.float().T
+    got = jq.f16_matmul(gpu, x.cuda(), wt.cuda()).cpu()
+    assert (want - got).abs().max().item() <= want[0, 0].abs().item() * 1e-3
+
+
+# ------------------------------------------------------------------ host-side rejection
+
+def test_bad_shapes_and_lengths_are_rejected(gpu):
+    raw = synth.weights(jq.Q4K, 1, 64, 256)
+    with pytest.raises(jq.JvError, match=r"Q4K \[1x64, 256\] has the wrong byte count"):
+        jq.QMatrix.upload(gpu, jq.Q4K, 64, 256, 1, raw[:-1])
+    with pytest.raises(jq.JvError, match="unsupported type"):
+        jq.QMatrix.upload(gpu, 2, 64, 256, 1, raw)
+    with pytest.raises(jq.JvError, match=r"Q8_0 \[1x32, 256\] has an unsupported shape"):
+        jq.QMatrix.upload(gpu, jq.Q8_0, 32, 256, 1, synth.weights(jq.Q8_0, 1, 32, 256))
+    with pytest.raises(jq.JvError, match="F32 has no GPU block layout"):
+        jq.QMatrix.upload(gpu, jq.F32, 64, 64, 1, np.zeros(64 * 64 * 4, np.uint8))
+    w = jq.QMatrix.upload(gpu, jq.Q4K, 64, 256, 1, raw)
+    x = torch.zeros((4, 256), dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros((4, 64), dtype=torch.float32, device="cuda")
+    with pytest.raises(jq.JvError, match="too short"):
+        jq.matmul_plan(gpu, x, 5, w, out, None, jq.Plan(32, 64, 1))
+    with pytest.raises(jq.JvError, match="not valid"):
+        jq.matmul_plan(gpu, x, 4, w, out, None, jq.Plan(48, 64, 1))
+    with pytest.raises(jq.JvError, match="not valid"):
+        jq.matmul_plan(gpu, x, 4, w, out, None, jq.Plan(32, 128, 1))
+    with pytest.raises(jq.JvError, match="at most 16 rows"):
+        jq.matvec(gpu, torch.zeros((17, 256), dtype=torch.bfloat16, device="cuda"), 17, w,
+                  torch.zeros((17, 64), dtype=torch.float32, device="cuda"))
+    with pytest.raises(jq.JvError, match="scratch"):
+        jq.matmul_plan(gpu, x, 4, w, out, None, jq.Plan(32, 64, 2))
+    # m == 0 is a no-op (gemm.rs:1138, :1219)
+    jq.matmul_plan(gpu, x, 0, w, out, None, jq.Plan(32, 64, 1))
+
+
+def test_plan_rules_follow_the_reference(gpu):
+    w = jq.QMatrix.upload(gpu, jq.Q8_0, 256, 512, 1, synth.weights(jq.Q8_0, 1, 256, 512))
+    # Plan::heuristic (gemm.rs:987-1004)
+    assert jq.Plan.heuristic(w, 70, True, 160) == jq.Plan(64, 128, 1)
+    assert jq.Plan.heuristic(w, 2, False, 160) == jq.Plan(0, 128, 1)
+    assert jq.Plan.heuristic(w, 16, False, 160) == jq.Plan(32, 128, 2)
+    # valid_for (gemm.rs:1006-1015)
+    assert jq.Plan(0, 128, 1).valid_for(w, 16) and not jq.Plan(0, 128, 1).valid_for(w, 17)
+    assert not jq.Plan(0, 128, 2).valid_for(w, 4)
+    assert jq.Plan(128, 128, 8).valid_for(w, 4) and not jq.Plan(128, 128, 9).valid_for(w, 4)
+    assert not jq.Plan(128, 128, 0).valid_for(w, 4)
