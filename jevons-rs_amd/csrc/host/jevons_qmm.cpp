@@ -262,8 +262,18 @@ jv_status build_from_device(jv_ctx *ctx, uint32_t type, jv_fmt fmt, size_t n, si
     w->bytes = l.q + l.h + l.d;
     jv_status st = JV_OK;
     if (fmt == JV_FMT_Q4K) {
-        hipError_t e = hipMemcpy(base + oq, raw_dev, bytes, hipMemcpyDeviceToDevice);
-        if (e != hipSuccess) st = fail(JV_ERR_HIP, "hipMemcpy: %s", hipGetErrorString(e));
+        RepackParams rp{};
+        rp.raw = (const uint8_t *)raw_dev;
+        rp.wq = base + oq;
+        rp.chunks = (int64_t)blocks;
+        int32_t kblocks = (int32_t)(k / 256);
+        void *args[] = {&rp, &kblocks};
+        st = launch(ctx, "jv_repack_q4k", dim3((unsigned)((rp.chunks + 255) / 256)), dim3(256), 0,
+                    nullptr, args);
+        if (st == JV_OK) {
+            hipError_t e = hipDeviceSynchronize();
+            if (e != hipSuccess) st = fail(JV_ERR_HIP, "repack: %s", hipGetErrorString(e));
+        }
     } else {
         RepackParams rp{};
         rp.raw = (const uint8_t *)raw_dev;
@@ -331,6 +341,66 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
     if (!x || !out) return fail(JV_ERR_INVALID, "null activation or output buffer");
     if (((uintptr_t)x & 15u) != 0) return fail(JV_ERR_INVALID, "activations must be 16-byte aligned");
 
+    if (plan.bm == 0 && w->fmt == JV_FMT_Q4K && m <= 16 && getenv("JV_QMV2") &&
+        w->n * w->experts * w->k / 2 < (1ull << 32)) {
+        // Small-row Q4_K kernel, one workgroup per 16-row tile.
+        int waves = 4, pf = 4;
+        sscanf(getenv("JV_QMV2"), "%dx%d", &waves, &pf);
+        if (!((waves == 4 && pf == 4) || (waves == 8 && pf == 2))) { waves = 4; pf = 4; }
+        const int U = (int)(w->k / 256);
+        const int umax = (U + waves - 1) / waves;
+        const int refill = umax > pf ? 1 : 0;
+        const size_t lds = (size_t)waves * m * ((size_t)umax * 256 + 8) * 2 +
+                           (size_t)waves * m * umax * 8 * 4 + (size_t)waves * 64 * 16;
+        if (lds <= ctx->info.lds_bytes) {
+            QmmParams p{};
+            p.x = x;
+            p.out = out;
+            p.wq = w->q;
+            p.M = (int32_t)m;
+            p.N = (int32_t)w->n;
+            p.K = (int32_t)w->k;
+            p.ldx = (int32_t)w->k;
+            p.ldo = (int32_t)w->n;
+            p.act = (int32_t)act;
+            p.out_type = (int32_t)out_type;
+            p.splits = 1;
+            void *args[] = {&p};
+            char name[48];
+            snprintf(name, sizeof name, "jv_qmv2_q4k_w%d_p%d_m%d_r%d", waves, pf, m == 1 ? 1 : (m == 2 ? 2 : 4), refill);
+            return launch(ctx, name, dim3((unsigned)(w->n * w->experts / 16)), dim3((unsigned)(64 * waves)), lds, stream, args);
+        }
+    }
+    if (plan.bm == 0 && w->fmt == JV_FMT_Q4K && w->k <= 16384 && w->n * w->experts * w->k / 2 < (1ull << 32)) {
+        // Small-row Q4_K kernel: one 8-wave workgroup per compute unit stages the activations
+        // and their sub-block sums once and streams a contiguous range of 16-row tiles.
+        const int T = (int)(w->n / 16);
+        const int cus = std::max(1, ctx->info.compute_units);
+        int waves = 8, pf = 4, late = 0;
+        if (const char *e = getenv("JV_QMV_SHAPE")) sscanf(e, "%dx%dx%d", &waves, &pf, &late);
+        if (!((waves == 8 && (pf == 4 || pf == 8)) || (waves == 16 && pf == 4))) { waves = 8; pf = 4; }
+        late = late ? 1 : 0;
+        const size_t lds = m * (w->k + 8) * 2 + m * (w->k / 32) * 4 + (size_t)waves * 2 * 64 * 16;
+        if (lds <= ctx->info.lds_bytes) {
+            QmmParams p{};
+            p.x = x;
+            p.out = out;
+            p.wq = w->q;
+            p.M = (int32_t)m;
+            p.N = (int32_t)w->n;
+            p.K = (int32_t)w->k;
+            p.ldx = (int32_t)w->k;
+            p.ldo = (int32_t)w->n;
+            p.act = (int32_t)act;
+            p.out_type = (int32_t)out_type;
+            p.splits = 1;
+            const int grid = std::min(cus, T);
+            void *args[] = {&p};
+            char name[48];
+            snprintf(name, sizeof name, "jv_qmv_q4k_w%d_p%d_m%d_l%d", waves, pf, m == 1 ? 1 : (m == 2 ? 2 : 4), late);
+            return launch(ctx, name, dim3((unsigned)grid), dim3((unsigned)(64 * waves)), lds, stream, args);
+        }
+    }
     const int MT = plan_mt(plan), NT = plan_nt(plan);
     const int KU = fmt_unit(w->fmt);
     const int splits = (int)plan.splits;

@@ -27,6 +27,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../qmm_params.h"
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -38,6 +40,15 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kLdsPad = 8;  // FP16 elements of padding per staged activation row (16 bytes)
+
+// Workgroup barrier ordering LDS only. __syncthreads() fences every address space, which on
+// gfx950 waits for all outstanding global loads (vmcnt(0)) and so drains the weight prefetch
+// queued ahead of the barrier; this one waits for LDS traffic (lgkmcnt(0)) alone.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 __device__ __forceinline__ float h2f(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xffffu));
@@ -72,59 +83,69 @@ __device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *(const uint4 *
 //   frag_f32()  those 8 weights, decoded exactly as quant.rs does
 // ---------------------------------------------------------------------------------------------
 
-// Q4_K, device layout = the GGUF blocks unchanged: row-major [rows][K/256] x 144 bytes
-// (f16 d, f16 dmin, 12 scale bytes, 128 quant bytes). Lane group g holds pair g of the block
-// (quant bytes 32g..32g+31): step s = 4h + c covers bytes 8c..8c+7, nibble h, i.e. elements
-// 64g + 32h + 8c + e of sub-block 2g + h (quant.rs:25-41).
+// Q4_K, device layout: GGUF blocks (f16 d, f16 dmin, 12 scale bytes, 128 quant bytes) regrouped
+// per 16-row tile and block into 2304 contiguous bytes, tile-major then block:
+//   [0, 1024)     lane 16g + r: quant bytes 8g..8g+7 of pairs 0 and 1 of row r's block
+//   [1024, 2048)  lane 16g + r: the same bytes of pairs 2 and 3
+//   [2048, 2304)  the 16 rows' 16-byte heads (d, dmin, scales)
+// where pair p is quant bytes 32p..32p+31 and each 4-byte group is stored in the order
+// {0, 2, 1, 3}. Each 16-byte load of a wave reads 1 KB (or the 256-byte heads) contiguously.
+// Lane group g thus holds elements 32j + 8g + e of every sub-block j (low nibbles of pair j/2
+// for even j, high nibbles for odd j; quant.rs:25-41), and the {0, 2, 1, 3} order makes
+// (w & 0x000f000f) hold the nibbles of elements e, e+1 in its two 16-bit halves.
+__device__ __forceinline__ uint32_t q4k_nib(uint32_t w, int e, int h) {
+    // element e (0..3) of a stored word, nibble h: byte position {0, 2, 1, 3}[e]
+    const int pos = (e == 1) ? 2 : (e == 2 ? 1 : e);
+    return (w >> (8 * pos + 4 * h)) & 15u;
+}
+
+// (scale, min) of Q4_K sub-block j from the 12 scale bytes held in hd.y..hd.w (quant.rs:14-23)
+__device__ __forceinline__ void q4k_scale_min_dev(const uint4 &hd, int j, uint32_t &sc, uint32_t &mn) {
+    const int sh = 8 * (j & 3);
+    const uint32_t a = hd.y >> sh, b = hd.z >> sh, c = hd.w >> sh;
+    if (j < 4) {
+        sc = a & 63u;
+        mn = b & 63u;
+    } else {
+        sc = (c & 15u) | ((a >> 2) & 48u);
+        mn = ((c >> 4) & 15u) | ((b >> 2) & 48u);
+    }
+}
+
 struct FQ4K {
     static constexpr int KU = 256;
     struct Raw {
         uint4 hd, q0, q1;
     };
     struct Prep {
-        float dd[2], mm[2];
+        float dd[8], mm[8];
     };
     __device__ static void load(Raw &r, const uint8_t *wq, const uint8_t *, const uint8_t *,
                                 int K, int row, int u, int g) {
-        const uint8_t *blk = wq + ((size_t)row * (size_t)(K / 256) + (size_t)u) * 144u;
-        r.hd = ld16(blk);
-        r.q0 = ld16(blk + 16 + 32 * g);
-        r.q1 = ld16(blk + 32 + 32 * g);
+        const int rr = row & 15;
+        const uint8_t *tb = wq + ((size_t)(row >> 4) * (size_t)(K / 256) + (size_t)u) * 2304u;
+        r.q0 = ld16(tb + (16 * g + rr) * 16);
+        r.q1 = ld16(tb + 1024 + (16 * g + rr) * 16);
+        r.hd = ld16(tb + 2048 + rr * 16);
     }
-    // q4k_scale_min (quant.rs:14-23) for sub-blocks j = 2g and 2g + 1.
-    __device__ static void prep(const Raw &r, Prep &p, int g) {
+    __device__ static void prep(const Raw &r, Prep &p, int) {
         const float d = h2f(r.hd.x), dmin = h2f(r.hd.x >> 16);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int j = 2 * g + h;
-            const int jj = j & 3;
-            const uint32_t a = (r.hd.y >> (8 * jj)) & 0xffu;  // scale byte jj
-            const uint32_t b = (r.hd.z >> (8 * jj)) & 0xffu;  // scale byte jj + 4
-            const uint32_t c = (r.hd.w >> (8 * jj)) & 0xffu;  // scale byte jj + 8
+        for (int j = 0; j < 8; ++j) {
             uint32_t sc, mn;
-            if (j < 4) {
-                sc = a & 63u;
-                mn = b & 63u;
-            } else {
-                sc = (c & 15u) | ((a >> 6) << 4);
-                mn = (c >> 4) | ((b >> 6) << 4);
-            }
-            p.dd[h] = d * (float)sc;     // exact: 11 x 6 significant bits
-            p.mm[h] = dmin * (float)mn;  // exact
+            q4k_scale_min_dev(r.hd, j, sc, mn);
+            p.dd[j] = d * (float)sc;     // exact: 11 x 6 significant bits
+            p.mm[j] = dmin * (float)mn;  // exact
         }
     }
-    __device__ static int kidx(int s, int g) { return 64 * g + 32 * (s >> 2) + 8 * (s & 3); }
+    __device__ static int kidx(int s, int g) { return 32 * s + 8 * g; }
     __device__ static void frag_f32(const Raw &r, const Prep &p, int s, int, float v[8]) {
-        const int h = s >> 2, c = s & 3;
+        const int pr = s >> 1, h = s & 1;
         const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
-        const uint32_t ta = (w[2 * c] >> (4 * h)) & 0x0f0f0f0fu;
-        const uint32_t tb = (w[2 * c + 1] >> (4 * h)) & 0x0f0f0f0fu;
-        const float dd = p.dd[h], mm = p.mm[h];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < 8; ++e) {
             // d*s*q is exact, so one fused rounding equals quant.rs's product-then-subtract.
-            v[e] = __builtin_fmaf((float)((ta >> (8 * e)) & 0xffu), dd, -mm);
-            v[e + 4] = __builtin_fmaf((float)((tb >> (8 * e)) & 0xffu), dd, -mm);
+            v[e] = __builtin_fmaf((float)q4k_nib(w[2 * pr + (e >> 2)], e & 3, h), p.dd[s], -p.mm[s]);
         }
     }
 };
@@ -351,9 +372,9 @@ __device__ __forceinline__ void qmm_body(const QmmParams &p) {
         if ((u - u_first) % kc_units == 0) {
             chunk_u0 = u;
             const int kl = min(kc_units, u_last - u) * F::KU;
-            __syncthreads();
+            lds_barrier();
             stage_rows(p, lds, m0, rows_real, u * F::KU, kl, stride);
-            __syncthreads();
+            lds_barrier();
         }
         if (active) {
             if (u + 1 < u_last) {
@@ -442,7 +463,523 @@ __device__ __forceinline__ void dequant_body(const DequantParams &p) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Small-row Q4_K product (M <= 16) with exact integer weights.
+//
+// Per block and weight row, out += d * S - sum_j (1024 d + dmin m_j) X_j, where
+//   S   = sum_e x_e * (1024 + s_j q_e) over the block's 256 elements (one MFMA chain), the
+//         FP16 operand 1024 + s*q being exact (s <= 63, q <= 15) and built with one packed
+//         16-bit multiply-add on the bit pattern 0x6400 (= 1024.0);
+//   X_j = sum of the block's activations over sub-block j, prepared with the LDS staging;
+//   the correction is one FP32 MFMA 16x16x4 pair (k = sub-block).
+// This equals sum_e x_e * (d*s_j*q_e - dmin*m_j), the quant.rs:25-41 weights, up to FP32
+// rounding of the sums. Lane group g holds pair g of every block (sub-blocks 2g, 2g+1), so a
+// lane decodes two (scale, min) pairs per block. Activation fragments are stored in LDS with
+// each 8-element group in the order {0,2,1,3,4,6,5,7}, the order the nibble pairs come out of
+// a 32-bit word ((w & 0x000f000f) holds bytes 0 and 2).
+//
+// Each wave owns 16 weight rows over all of K; a workgroup of 4 waves owns 64 rows. Weight
+// loads run P blocks ahead of the MFMAs.
+// ---------------------------------------------------------------------------------------------
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_mad_u16(uint32_t a, uint32_t b, uint32_t c) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 r = __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b) + __builtin_bit_cast(u16x2, c);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// Loads are issued unconditionally (clamped to the last chunk) so the compiler can count
+// outstanding loads exactly and wait only for the ones it needs.
+template <int ACT, int NTHR, bool LATE, class After>
+__device__ __forceinline__ void stage_q4k_rows_act(const QmmParams &p, _Float16 *xs, float *Xs,
+                                                   After after) {
+    constexpr int XB = ACT == 2 ? 4 : 8;  // 16-byte loads per thread held at once
+    constexpr int EPL = ACT == 2 ? 4 : 8;  // elements per load
+    const int per_row = p.K >> 3;
+    const int total = p.M * per_row;  // 8-element chunks; multiple of 4 (K % 64 == 0)
+    const int stride = p.K + kLdsPad;
+    constexpr int nthr = NTHR;
+    bool issued = false;
+    for (int i0 = 0; i0 < total; i0 += XB * nthr) {
+        uint4 raw[XB][8 / EPL];
+        const int nq = min(XB, (total - i0 + nthr - 1) / nthr);  // batches with real chunks
+#pragma unroll
+        for (int q = 0; q < XB; ++q) {
+            if (q >= nq) break;  // uniform: later batches hold no chunk for any thread
+            const int i = min(i0 + q * nthr + (int)threadIdx.x, total - 1);
+            const int r = i / per_row;
+            const int c8 = i - r * per_row;
+            const size_t src = (size_t)r * (size_t)p.ldx + (size_t)(8 * c8);
+#pragma unroll
+            for (int hh = 0; hh < 8 / EPL; ++hh) {
+                if (ACT == 2)
+                    raw[q][hh] = *(const uint4 *)((const float *)p.x + src + 4 * hh);
+                else
+                    raw[q][hh] = *(const uint4 *)((const uint16_t *)p.x + src);
+            }
+        }
+        if (!issued && !LATE) {
+            after();
+            issued = true;
+        }
+#pragma unroll
+        for (int q = 0; q < XB; ++q) {
+            if (q >= nq) break;
+            const int i = i0 + q * nthr + (int)threadIdx.x;
+            float part = 0.f;
+            int r = 0, c8 = 0;
+            if (i < total) {
+                r = i / per_row;
+                c8 = i - r * per_row;
+                float v[8];
+                if (ACT == 2) {
+                    const uint32_t w[8] = {raw[q][0].x, raw[q][0].y, raw[q][0].z, raw[q][0].w,
+                                           raw[q][8 / EPL - 1].x, raw[q][8 / EPL - 1].y,
+                                           raw[q][8 / EPL - 1].z, raw[q][8 / EPL - 1].w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = __builtin_bit_cast(float, w[e]);
+                } else {
+                    const uint32_t w[4] = {raw[q][0].x, raw[q][0].y, raw[q][0].z, raw[q][0].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[2 * e] = ACT == 0 ? h2f(w[e]) : bf2f(w[e]);
+                        v[2 * e + 1] = ACT == 0 ? h2f(w[e] >> 16) : bf2f(w[e] >> 16);
+                    }
+                }
+                f16x8 h;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = (_Float16)v[e];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) part += (float)h[e];
+                *(f16x8 *)(xs + r * stride + 8 * c8) = h;
+            }
+            // four consecutive 8-element chunks (lanes 4j..4j+3) form one 32-element sub-block
+            part += __shfl_xor(part, 1);
+            part += __shfl_xor(part, 2);
+            if (i < total && (c8 & 3) == 0) Xs[r * (p.K >> 5) + (c8 >> 2)] = part;
+        }
+    }
+    if (!issued) after();
+}
+
+// Stages activation rows [0, M) x [0, K) as FP16 plus FP32 sums over each 32-element
+// sub-block (xs row stride K + 8 elements, Xs row stride K / 32). The activation loads are issued
+// first and `after()` (the weight loads) next, so the activations do not queue behind the
+// weight stream.
+// LATE: `after()` runs once the activations are converted instead of right after their loads.
+template <int NTHR, bool LATE, class After>
+__device__ __forceinline__ void stage_q4k_rows_first(const QmmParams &p, _Float16 *xs, float *Xs,
+                                                     After after) {
+    if (p.act == 0)
+        stage_q4k_rows_act<0, NTHR, LATE>(p, xs, Xs, after);
+    else if (p.act == 1)
+        stage_q4k_rows_act<1, NTHR, LATE>(p, xs, Xs, after);
+    else
+        stage_q4k_rows_act<2, NTHR, LATE>(p, xs, Xs, after);
+}
+
+// Q4_K (scale, min) of sub-blocks 2g and 2g+1, branch-free (quant.rs:14-23): lane groups
+// 0-1 hold sub-blocks 0-3 (low form), groups 2-3 sub-blocks 4-7 (high form).
+__device__ __forceinline__ void q4k_pair_scales(const uint4 &hd, int g, uint32_t sc[2], uint32_t mn[2]) {
+    const bool hi = g >= 2;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int sh = 16 * (g & 1) + 8 * h;  // 8 * ((2g + h) & 3)
+        const uint32_t a = hd.y >> sh, b = hd.z >> sh, c = hd.w >> sh;
+        const uint32_t sc_lo = a & 63u, mn_lo = b & 63u;
+        const uint32_t sc_hi = (c & 15u) | ((a >> 2) & 48u);
+        const uint32_t mn_hi = ((c >> 4) & 15u) | ((b >> 2) & 48u);
+        sc[h] = hi ? sc_hi : sc_lo;
+        mn[h] = hi ? mn_hi : mn_lo;
+    }
+}
+
+// One Q4_K block of a 16-row tile as one lane holds it: quant bytes as FQ4K::load reads them,
+// and one dword of the heads instead of a whole head. Lane 16g + r loads dword g of row r's
+// 16-byte head, so the wave reads the 256 head bytes once (a 16-byte load replicated over the
+// four lane groups costs about as much load bandwidth as 1 KB of quants).
+struct Q4KItem {
+    uint4 q0, q1;
+    uint32_t hv;
+};
+
+__device__ __forceinline__ void q4k_item_load(Q4KItem &it, const uint8_t *wq, int K, int tile,
+                                              int u, int g, int r) {
+    const uint8_t *tb = wq + ((size_t)tile * (size_t)(K / 256) + (size_t)u) * 2304u;
+    it.q0 = ld16(tb + (16 * g + r) * 16);
+    it.q1 = ld16(tb + 1024 + (16 * g + r) * 16);
+    it.hv = *(const uint32_t *)(tb + 2048 + r * 16 + 4 * g);
+}
+
+// All four head dwords of row r in every lane group, from lane 16g + r holding dword g.
+// permlane16_swap exchanges odd 16-lane rows of its first operand with even rows of its
+// second; permlane32_swap exchanges the upper 32 lanes of the first with the lower 32 of the
+// second (gfx950).
+__device__ __forceinline__ uint4 q4k_head_gather(uint32_t hv) {
+    const auto x = __builtin_amdgcn_permlane16_swap(hv, hv, false, false);  // {d0,d0,d2,d2}, {d1,d1,d3,d3}
+    const auto e = __builtin_amdgcn_permlane32_swap(x[0], x[0], false, false);  // d0, d2 everywhere
+    const auto o = __builtin_amdgcn_permlane32_swap(x[1], x[1], false, false);  // d1, d3 everywhere
+    return uint4{(uint32_t)e[0], (uint32_t)o[0], (uint32_t)e[1], (uint32_t)o[1]};
+}
+
+// One Q4_K block of 16 weight rows against the staged activations: acc += products.
+// Sub-block j is one MFMA on exact operands 1024 + q (even j, low nibbles, bits 0-3) or
+// 1024 + 16 q (odd j, high nibbles, bits 4-7), each built with a single and-or on the bit
+// pattern 0x6400 (= 1024.0); S_j is scaled by A'_j = d s_j (/16 for odd j) and the bias and
+// min terms sum_j (1024 A'_j + dmin m_j) X_j come from one FP32 MFMA 16x16x4 pair, where
+// X_j is the sub-block's activation sum. This equals the quant.rs:25-41 weights times x, up
+// to FP32 rounding of the sums. Lane group g decodes sub-blocks 2g, 2g+1 and reads the other
+// scales from their lane groups with ds_bpermute. Only output rows 4g + i, i < MV, are kept.
+template <int MV>
+__device__ __forceinline__ void q4k_block_v6(const Q4KItem &cur, const _Float16 *xrow,
+                                             const float *Xrow, int u, int g, int r16, f32x4 &acc) {
+    const uint4 hd = q4k_head_gather(cur.hv);
+    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+    uint32_t sc[2], mn[2];
+    q4k_pair_scales(hd, g, sc, mn);
+    const float a0 = d * (float)sc[0];              // A'_{2g}
+    const float a1 = d * (float)sc[1] * 0.0625f;    // A'_{2g+1}: high nibbles carry 16 q
+    const float c0 = -__builtin_fmaf(1024.f, a0, dmin * (float)mn[0]);
+    const float c1 = -__builtin_fmaf(1024.f, a1, dmin * (float)mn[1]);
+    float aj[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int src = ((j >> 1) * 16 + r16) * 4;
+        aj[j] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                              src, __builtin_bit_cast(int, (j & 1) ? a1 : a0)));
+    }
+    const uint32_t w[8] = {cur.q0.x, cur.q0.y, cur.q0.z, cur.q0.w, cur.q1.x, cur.q1.y, cur.q1.z, cur.q1.w};
+    const int kb = u * 256 + 8 * g;
+    // The magic held in a register lets each operand word be one v_and_or_b32 (a VOP3 op
+    // cannot encode two 32-bit literals on this architecture).
+    uint32_t magic = 0x64006400u;
+    asm volatile("" : "+v"(magic));
+    // All eight sub-block products are independent: issue every MFMA into its own result
+    // registers first and scale afterwards, so the matrix unit runs them back to back.
+    f32x4 S[8];
+#pragma unroll
+    for (int pr = 0; pr < 4; ++pr) {
+        const uint32_t wa = w[2 * pr], wb = w[2 * pr + 1];
+        const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int j = 2 * pr + h;
+            const uint32_t mask = h ? 0x00f000f0u : 0x000f000fu;
+            uint4 bq;
+            bq.x = (wa & mask) | magic;
+            bq.y = (wa8 & mask) | magic;
+            bq.z = (wb & mask) | magic;
+            bq.w = (wb8 & mask) | magic;
+            const f16x8 a = *(const f16x8 *)(xrow + kb + 32 * j);
+            S[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                a, __builtin_bit_cast(f16x8, bq), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < MV; ++i) acc[i] = __builtin_fmaf(aj[j], S[j][i], acc[i]);
+    // bias and min terms: k index = lane group g, sub-block 2g + t
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[u * 8 + 2 * g], c0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[u * 8 + 2 * g + 1], c1, acc, 0, 0, 0);
+}
+
+// Persistent small-row Q4_K kernel. Workgroup c (one per compute unit, W waves) owns tiles
+// [c*T/G, (c+1)*T/G) of 16 weight rows. Their (tile, block) list, tile-major, is cut into W
+// contiguous slices, one per wave. The activations are staged first; then each wave streams
+// its slice with its weight loads P blocks ahead of the MFMAs. Loads are unconditional (past
+// the slice end a slot reloads the slice's last block) so waits are exact. A wave writes the
+// tiles it covers completely; a tile cut between waves leaves partials in LDS that the wave
+// where the tile starts sums in wave order, so results are deterministic and independent of M.
+template <int W, int P, int MV, bool LATE>
+__device__ __forceinline__ void qmv_q4k_body(const QmmParams &p) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4;
+    const int r16 = lane & 15;
+    const int U = p.K >> 8;
+    const int T = p.N >> 4;
+    const int t_begin = (int)((int64_t)blockIdx.x * T / gridDim.x);
+    const int t_end = (int)((int64_t)(blockIdx.x + 1) * T / gridDim.x);
+    const int n_items = (t_end - t_begin) * U;
+    const int a = wave * n_items / W, b = (wave + 1) * n_items / W;
+    const int stride = p.K + kLdsPad;
+    _Float16 *xs = lds;
+    float *Xs = (float *)(lds + p.M * stride);
+    f32x4 *part = (f32x4 *)(Xs + p.M * (p.K >> 5));  // [W][2][64]
+
+    // item idx of the slice (clamped to its last item; an empty slice loads item 0)
+    auto load_item = [&](Q4KItem &dst, int idx) {
+        idx = b > a ? min(idx, b - 1) : 0;
+        q4k_item_load(dst, p.wq, p.K, t_begin + idx / U, idx % U, g, r16);
+    };
+    Q4KItem buf[P];
+    stage_q4k_rows_first<64 * W, LATE>(p, xs, Xs, [&] {
+#pragma unroll
+        for (int j = 0; j < P; ++j) load_item(buf[j], a + j);
+    });
+    lds_barrier();
+
+    const int arow = min(r16, p.M - 1);  // rows >= M feed output rows that are never stored
+    const _Float16 *xrow = xs + arow * stride;
+    const float *Xrow = Xs + arow * (p.K >> 5);
+
+    auto store = [&](int tile, const f32x4 &v) {
+        const int col = tile * 16 + r16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * g + i;
+            if (m < p.M) {
+                const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
+                if (p.out_type == 0)
+                    ((float *)p.out)[o] = v[i];
+                else
+                    ((uint16_t *)p.out)[o] = (uint16_t)f2bf(v[i]);
+            }
+        }
+    };
+
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    int nparts = 0;
+    int u = a % U, trel = a / U;  // block and tile (relative) of the current item
+    for (int i0 = a; i0 < b; i0 += P) {
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            const int idx = i0 + j;
+            if (idx < b) {
+                q4k_block_v6<MV>(buf[j], xrow, Xrow, u, g, r16, acc);
+                if (u == U - 1 || idx == b - 1) {  // end of this wave's share of a tile
+                    if (idx - u >= a && u == U - 1) {
+                        store(t_begin + trel, acc);
+                    } else {
+                        part[(wave * 2 + nparts) * 64 + lane] = acc;
+                        ++nparts;
+                    }
+                    acc = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+                if (++u == U) {
+                    u = 0;
+                    ++trel;
+                }
+            }
+            load_item(buf[j], idx + P);  // refill the freed slot P items ahead
+        }
+    }
+    lds_barrier();
+    // A tile cut between waves starts in one slice (the wave's tail partial) and continues as
+    // the first partial of the following waves. The wave where it starts combines it.
+    if (a < b) {
+        const int last_tile = (b - 1) / U;
+        if ((b - 1) % U != U - 1 && last_tile * U >= a) {
+            const int tail = (a % U) != 0 ? 1 : 0;  // a head partial comes first
+            f32x4 sum = part[(wave * 2 + tail) * 64 + lane];
+            const int tile_end = (last_tile + 1) * U;
+            for (int w = wave + 1; w < W; ++w) {
+                const int wa = w * n_items / W, wb = (w + 1) * n_items / W;
+                if (wa >= tile_end) break;
+                if (wa < wb) {
+                    const f32x4 v = part[(w * 2) * 64 + lane];  // w's first partial
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) sum[i] += v[i];
+                }
+            }
+            store(t_begin + last_tile, sum);
+        }
+    }
+}
+
+// Stages columns [c0, c0 + ncols) of activation rows [0, M) for one wave: FP16 into
+// xs[r * stride + c] and FP32 sums of each 32-column sub-block into Xs[r * xstride + c / 32].
+// The wave's first XB 16-byte loads per lane are issued before `after()` (the weight loads),
+// so waiting for them does not wait for the weights; later batches, if any, come after.
+template <int ACT, int XB, class After>
+__device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int ncols, _Float16 *xs,
+                                                int stride, float *Xs, int xstride, int lane,
+                                                After after) {
+    constexpr int EPL = ACT == 2 ? 4 : 8;  // elements per 16-byte load
+    constexpr int LPC = 8 / EPL;           // loads per 8-element chunk
+    constexpr int XC = XB / LPC;           // chunks held per lane at once
+    const int per_row = ncols >> 3;
+    const int total = p.M * per_row;  // 8-element chunks; a multiple of 4 (ncols % 32 == 0)
+    bool issued = false;
+    for (int i0 = 0; i0 < total; i0 += XC * 64) {
+        uint4 raw[XC][LPC];
+        const int nq = min(XC, (total - i0 + 63) >> 6);  // uniform: batches holding real chunks
+#pragma unroll
+        for (int q = 0; q < XC; ++q) {
+            if (q >= nq) break;
+            const int i = min(i0 + q * 64 + lane, total - 1);
+            const int r = i / per_row;
+            const int c8 = i - r * per_row;
+            const size_t src = (size_t)r * (size_t)p.ldx + (size_t)(c0 + 8 * c8);
+#pragma unroll
+            for (int hh = 0; hh < LPC; ++hh) {
+                if (ACT == 2)
+                    raw[q][hh] = *(const uint4 *)((const float *)p.x + src + 4 * hh);
+                else
+                    raw[q][hh] = *(const uint4 *)((const uint16_t *)p.x + src);
+            }
+        }
+        if (!issued) {
+            after();
+            issued = true;
+        }
+#pragma unroll
+        for (int q = 0; q < XC; ++q) {
+            if (q >= nq) break;
+            const int i = i0 + q * 64 + lane;
+            float part = 0.f;
+            int r = 0, c8 = 0;
+            if (i < total) {
+                r = i / per_row;
+                c8 = i - r * per_row;
+                float v[8];
+                if (ACT == 2) {
+#pragma unroll
+                    for (int hh = 0; hh < LPC; ++hh) {
+                        v[4 * hh + 0] = __builtin_bit_cast(float, raw[q][hh].x);
+                        v[4 * hh + 1] = __builtin_bit_cast(float, raw[q][hh].y);
+                        v[4 * hh + 2] = __builtin_bit_cast(float, raw[q][hh].z);
+                        v[4 * hh + 3] = __builtin_bit_cast(float, raw[q][hh].w);
+                    }
+                } else {
+                    const uint32_t w[4] = {raw[q][0].x, raw[q][0].y, raw[q][0].z, raw[q][0].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[2 * e] = ACT == 0 ? h2f(w[e]) : bf2f(w[e]);
+                        v[2 * e + 1] = ACT == 0 ? h2f(w[e] >> 16) : bf2f(w[e] >> 16);
+                    }
+                }
+                f16x8 h;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = (_Float16)v[e];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) part += (float)h[e];
+                *(f16x8 *)(xs + r * stride + 8 * c8) = h;
+            }
+            // lanes 4q..4q+3 hold the four 8-element chunks of one 32-element sub-block
+            part += __shfl_xor(part, 1);
+            part += __shfl_xor(part, 2);
+            if (i < total && (c8 & 3) == 0) Xs[r * xstride + (c8 >> 2)] = part;
+        }
+    }
+    if (!issued) after();
+}
+
+// Small-row Q4_K kernel, one workgroup per 16-row tile. Wave w of W owns blocks
+// [w U / W, (w+1) U / W) of the tile (U = K / 256): it issues its activation loads, then its
+// first P weight blocks, stages its own activation columns in a private LDS region (no
+// workgroup barrier), and runs the blocks as they arrive, refilling P blocks ahead when
+// REFILL. The W partial sums are added in wave order by wave 0, so results are deterministic
+// and each output row is independent of M. Many short workgroups, each reading one contiguous
+// 16-row tile, keep the HBM queues fuller than long-lived per-CU workgroups do.
+template <int W, int P, int MV, int XB, bool REFILL>
+__device__ __forceinline__ void qmv2_q4k_body(const QmmParams &p) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4;
+    const int r16 = lane & 15;
+    const int U = p.K >> 8;
+    const int tile = blockIdx.x;
+    const int u0 = wave * U / W;
+    const int nu = (wave + 1) * U / W - u0;
+    const int umax = (U + W - 1) / W;
+    const int stride = umax * 256 + kLdsPad;
+    const int xstride = umax * 8;
+    _Float16 *xs = lds + wave * p.M * stride;
+    float *Xall = (float *)(lds + W * p.M * stride);
+    float *Xs = Xall + wave * p.M * xstride;
+    f32x4 *part = (f32x4 *)(Xall + W * p.M * xstride);  // [W][64]
+
+    auto load_item = [&](Q4KItem &dst, int idx) {
+        q4k_item_load(dst, p.wq, p.K, tile, u0 + min(idx, nu - 1), g, r16);
+    };
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (nu > 0) {
+        Q4KItem buf[P];
+        auto issue = [&] {
+#pragma unroll
+            for (int j = 0; j < P; ++j) load_item(buf[j], j);
+        };
+        if (p.act == 0)
+            stage_wave_cols<0, XB>(p, u0 * 256, nu * 256, xs, stride, Xs, xstride, lane, issue);
+        else if (p.act == 1)
+            stage_wave_cols<1, XB>(p, u0 * 256, nu * 256, xs, stride, Xs, xstride, lane, issue);
+        else
+            stage_wave_cols<2, XB>(p, u0 * 256, nu * 256, xs, stride, Xs, xstride, lane, issue);
+        // LDS operations of one wave complete in order; this keeps the compiler from moving
+        // the fragment reads above the staging writes.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+        const int arow = min(r16, p.M - 1);  // rows >= M feed output rows that are never stored
+        const _Float16 *xrow = xs + arow * stride;
+        const float *Xrow = Xs + arow * xstride;
+        if (REFILL) {
+            for (int i0 = 0; i0 < nu; i0 += P) {
+#pragma unroll
+                for (int j = 0; j < P; ++j) {
+                    const int idx = i0 + j;
+                    if (idx < nu) q4k_block_v6<MV>(buf[j], xrow, Xrow, idx, g, r16, acc);
+                    load_item(buf[j], idx + P);
+                }
+            }
+        } else {  // nu <= P: every block is already in flight
+#pragma unroll
+            for (int j = 0; j < P; ++j)
+                if (j < nu) q4k_block_v6<MV>(buf[j], xrow, Xrow, j, g, r16, acc);
+        }
+    }
+    if (wave > 0) part[wave * 64 + lane] = acc;
+    lds_barrier();
+    if (wave == 0) {
+        for (int w = 1; w < W; ++w) {
+            const f32x4 v = part[w * 64 + lane];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += v[i];
+        }
+        const int col = tile * 16 + r16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * g + i;
+            if (m < p.M) {
+                const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
+                if (p.out_type == 0)
+                    ((float *)p.out)[o] = acc[i];
+                else
+                    ((uint16_t *)p.out)[o] = (uint16_t)f2bf(acc[i]);
+            }
+        }
+    }
+}
+
 }  // namespace
+
+#define JV_QMV2(W, P, MV, XB, R)                                                              \
+    extern "C" __global__ __launch_bounds__(64 * W) void jv_qmv2_q4k_w##W##_p##P##_m##MV##_r##R( \
+        QmmParams p) {                                                                        \
+        qmv2_q4k_body<W, P, MV, XB, R == 1>(p);                                               \
+    }
+#define JV_QMV2_M(W, P, R) JV_QMV2(W, P, 1, 2, R) JV_QMV2(W, P, 2, 4, R) JV_QMV2(W, P, 4, 8, R)
+JV_QMV2_M(4, 4, 0)
+JV_QMV2_M(4, 4, 1)
+JV_QMV2_M(8, 2, 0)
+JV_QMV2_M(8, 2, 1)
+
+#define JV_QMV(W, P, MV, L)                                                                \
+    extern "C" __global__ __launch_bounds__(64 * W) void jv_qmv_q4k_w##W##_p##P##_m##MV##_l##L( \
+        QmmParams p) {                                                                        \
+        qmv_q4k_body<W, P, MV, L == 1>(p);                                                    \
+    }
+#define JV_QMV_M(W, P, L) JV_QMV(W, P, 1, L) JV_QMV(W, P, 2, L) JV_QMV(W, P, 4, L)
+JV_QMV_M(8, 4, 0)
+JV_QMV_M(8, 8, 0)
+JV_QMV_M(8, 4, 1)
+JV_QMV_M(8, 8, 1)
+JV_QMV_M(16, 4, 0)
+JV_QMV_M(16, 4, 1)
 
 // ---------------------------------------------------------------------------------------------
 // Entry points (looked up by name with hipModuleGetFunction).
@@ -499,6 +1036,29 @@ extern "C" __global__ __launch_bounds__(256) void jv_reduce_splits(const float *
 // ---------------------------------------------------------------------------------------------
 // Repack GGML blocks (device copy) into the device layouts above.
 // ---------------------------------------------------------------------------------------------
+
+// One work item per Q4_K block row: 144 raw bytes -> its pieces of the tile layout.
+extern "C" __global__ __launch_bounds__(256) void jv_repack_q4k(RepackParams p, int32_t kblocks) {
+    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;  // row * kblocks + u
+    if (b >= p.chunks) return;
+    const int64_t row = b / kblocks;
+    const int64_t u = b - row * kblocks;
+    const int rr = (int)(row & 15);
+    const uint8_t *src = p.raw + b * 144;
+    uint8_t *tb = p.wq + ((row >> 4) * kblocks + u) * 2304;
+    *(uint4 *)(tb + 2048 + rr * 16) = *(const uint4 *)src;
+    const int order[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    for (int g = 0; g < 4; ++g) {
+        uint8_t piece[32];
+        for (int pr = 0; pr < 4; ++pr)
+            for (int e = 0; e < 8; ++e) piece[8 * pr + e] = src[16 + 32 * pr + 8 * g + order[e]];
+        uint8_t *d0 = tb + (16 * g + rr) * 16, *d1 = tb + 1024 + (16 * g + rr) * 16;
+        for (int e = 0; e < 16; ++e) {
+            d0[e] = piece[e];
+            d1[e] = piece[16 + e];
+        }
+    }
+}
 
 // One work item per Q6_K block: 210 raw bytes -> 208 layout bytes + FP16 scale.
 extern "C" __global__ __launch_bounds__(256) void jv_repack_q6k(RepackParams p) {

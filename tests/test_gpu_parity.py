@@ -91,8 +91,10 @@ def test_every_plan_matches_oracle_and_tiles_are_row_invariant(gpu, name, type_i
     n, k = 256, 512
     w, raw = make_matrix(gpu, type_id, n, k, seed=7)
     scratch = jq.SplitScratch(gpu)
+    gemv_rows = {}
+    x_all = synth.normal_rows(100, 150, k)
     for m in (1, 3, 16, 70, 150):
-        x32 = synth.normal_rows(100 + m, m, k)
+        x32 = x_all[:m]
         x, xv = activations(act, x32)
         if act == "f32":
             xv = xv.astype(np.float16).astype(np.float32)  # the kernels stage FP16 activations
@@ -105,11 +107,16 @@ def test_every_plan_matches_oracle_and_tiles_are_row_invariant(gpu, name, type_i
             got = out.cpu().numpy()
             e = err(got, want)
             assert e <= TOL, f"m={m} {plan}: normalized error {e:.2e}"
-            if plan.splits == 1:
+            if plan.bm == 0:
+                gemv_rows[m] = got
+            elif plan.splits == 1:
                 if reference is None:
                     reference = got
                 else:
                     assert np.array_equal(reference, got), f"m={m} {plan} is not row invariant"
+    # the small-row kernel computes each row independently of the others
+    assert np.array_equal(gemv_rows[1], gemv_rows[3][:1])
+    assert np.array_equal(gemv_rows[3], gemv_rows[16][:3])
 
 
 def test_reference_dense_plan_recipe(gpu):
@@ -173,7 +180,7 @@ def test_q4k_decode_gemv_full_shape(gpu, m):
 
 def test_q4k_prefill_gemm_m512_rows(gpu):
     """Q4_K GEMM M=512, K=3840, N=15360 with 1% outlier columns: 48 sampled rows against the
-    f64 oracle, and every row bitwise equal to the row-invariant small-row plan's."""
+    f64 oracle, and rows bitwise equal to another row-invariant plan's on a 16-row slice."""
     m, n, k = 512, 15360, 3840
     say("q4k gemm", m, n, k)
     w, raw = make_matrix(gpu, jq.Q4K, n, k, seed=2)
@@ -190,7 +197,7 @@ def test_q4k_prefill_gemm_m512_rows(gpu):
     assert e <= TOL
     for r0 in (0, 200, 496):
         o1 = torch.empty((16, n), dtype=torch.float32, device="cuda")
-        jq.matmul_plan(gpu, x[r0:r0 + 16].contiguous(), 16, w, o1, None, jq.Plan(0, 64, 1))
+        jq.matmul_plan(gpu, x[r0:r0 + 16].contiguous(), 16, w, o1, None, jq.Plan(32, 64, 1))
         assert torch.equal(o1, out[r0:r0 + 16]), r0
 
 
