@@ -6,13 +6,19 @@ out), each on a different copy of the weights: the copies rotate through more th
 their wall time (HIP graph replay, inputs resident in HBM). The Q4_K prefill GEMM (M = 512, 1%
 outlier columns) is timed the same way and reported under "gemm".
 
-Roofline entries use the kernels' own durations: each launch is bracketed by events on its own
-stream while the stream is held behind a spin kernel, so the host never starves the queue.
+Roofline entries use each kernel's average launch duration: one HIP graph of R back-to-back
+launches per kernel, replayed between two events recorded on the stream the graph runs on,
+divided by R (the device runs the launches back to back, so this tracks the kernel-trace
+durations of rocprofv3).
 
 CPU baseline: the oracle's port of the reference CPU path (quant.rs decode + f32-accumulate
 matmul, OpenMP) on the same Q4_K matrix at M = 1, timed on this host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+HBM traffic: two rocprofv3 --pmc passes over a short run of the same launches (FETCH_SIZE, then
+WRITE_SIZE, KiB per dispatch), each scaled by what the counter reads in the same pass for a
+device-to-device copy of the same byte count, whose traffic is known.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-traffic]
 """
 from __future__ import annotations
 
@@ -20,7 +26,13 @@ import argparse
 import json
 import math
 import os
+import shutil
+import signal
+import sqlite3
+import statistics
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -38,22 +50,24 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def kernel_times_ms(fn_list, reps):
-    """Average GPU duration of each callable's launch, measured with events that bracket one
-    launch each while the stream is held behind a spin kernel."""
+def kernel_time_ms(fn, reps):
+    """Average duration of one launch of `fn(i)`: a graph of `reps` launches replayed between
+    two events on the replay stream."""
     import torch
 
-    starts = [[torch.cuda.Event(enable_timing=True) for _ in range(reps)] for _ in fn_list]
-    ends = [[torch.cuda.Event(enable_timing=True) for _ in range(reps)] for _ in fn_list]
-    torch.cuda.synchronize()
-    torch.cuda._sleep(50_000_000)  # holds the stream while the host queues the launches
-    for r in range(reps):
-        for j, fn in enumerate(fn_list):
-            starts[j][r].record()
-            fn(r)
-            ends[j][r].record()
-    torch.cuda.synchronize()
-    return [sum(s.elapsed_time(e) for s, e in zip(starts[j], ends[j])) / reps for j in range(len(fn_list))]
+    g = graph_of(fn, reps)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        g.replay()  # warm
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(s)
+        g.replay()
+        t1.record(s)
+    t1.synchronize()
+    torch.cuda.current_stream().wait_stream(s)
+    return t0.elapsed_time(t1) / reps
 
 
 def graph_of(fn, count):
@@ -68,6 +82,103 @@ def graph_of(fn, count):
                 fn(i)
     torch.cuda.current_stream().wait_stream(s)
     return g
+
+
+GEMV_N, GEMV_K, GEMV_MS = 15360, 3840, (1, 4, 8)
+
+
+def pmc_child():
+    """Launch workload of the traffic passes: each GEMV launch 20 times on rotating weight copies,
+    then a device copy of the weight byte count 20 times."""
+    import numpy as np
+    import torch
+
+    import jevons_qmm as jq
+    from jevons_qmm import synth
+
+    n, k = GEMV_N, GEMV_K
+    gpu = jq.Gpu(0)
+    raw = synth.weights(jq.Q4K, 2, n, k)
+    raw_dev = torch.from_numpy(raw).cuda()
+    copies = max(2, math.ceil(ROTATION_BYTES / raw.size))
+    mats = [jq.QMatrix.upload_device(gpu, jq.Q4K, n, k, 1, raw_dev) for _ in range(copies)]
+    x8 = synth.normal_rows(21, 8, k)
+    xb = torch.from_numpy(synth.to_bf16(x8).view(np.int16).copy()).view(torch.bfloat16).cuda()
+    for m in GEMV_MS:
+        xm = xb[:m].contiguous()
+        out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        for r in range(20):
+            jq.matmul(gpu, xm, m, mats[r % copies], out)
+        torch.cuda.synchronize()
+    srcs = [torch.empty(raw.size, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+    dst = torch.empty(raw.size, dtype=torch.uint8, device="cuda")
+    for r in range(20):
+        dst.copy_(srcs[r % copies])
+    torch.cuda.synchronize()
+    print("pmc child done", flush=True)
+
+
+def _pmc_pass(counter, workdir):
+    """One rocprofv3 pass of `counter` over the child workload -> {kernel name: [values]}."""
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    out = os.path.join(workdir, counter)
+    cmd = [prof, "--pmc", counter, "-d", out, "-o", "run", "--", sys.executable,
+           os.path.abspath(__file__), "--pmc-child"]
+    proc = subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                            start_new_session=True, env=dict(os.environ, TMPDIR=workdir))
+    try:
+        text = proc.communicate(timeout=150)[0].decode(errors="replace")
+    except subprocess.TimeoutExpired:
+        os.killpg(proc.pid, signal.SIGKILL)
+        proc.communicate()
+        raise RuntimeError(f"rocprofv3 --pmc {counter} timed out")
+    if "pmc child done" not in text:
+        raise RuntimeError(f"rocprofv3 --pmc {counter} failed: {text[-400:]}")
+    dbs = [os.path.join(r, f) for r, _, fs in os.walk(out) for f in fs if f.endswith("_results.db")]
+    if not dbs:
+        raise RuntimeError(f"rocprofv3 --pmc {counter} wrote no database")
+    vals = {}
+    for db in dbs:
+        con = sqlite3.connect(db)
+        for name, lds, v in con.execute(
+                "select kernel_name, lds_block_size, value from counters_collection "
+                "where counter_name = ?", (counter,)):
+            # the LDS size tells launches of one kernel at different m apart
+            vals.setdefault(f"{name}@lds{lds}" if name.startswith("jv_") else name, []).append(v)
+        con.close()
+    return vals
+
+
+def measure_traffic(wbytes):
+    """HBM bytes per launch of each GEMV kernel, from FETCH_SIZE and WRITE_SIZE scaled by the
+    same counters' reading for a device copy of `wbytes` bytes."""
+    workdir = tempfile.mkdtemp(prefix="jv_pmc_")
+    try:
+        res = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            vals = _pmc_pass(counter, workdir)
+            copy = [v for name, vs in vals.items() if "copyBuffer" in name for v in vs]
+            kern = {name: statistics.median(vs) for name, vs in vals.items() if name.startswith("jv_")}
+            if not copy or not kern:
+                raise RuntimeError(f"{counter}: no copy or product dispatches recorded")
+            kib_copy = statistics.median(copy)
+            factor = wbytes / (kib_copy * 1024.0)
+            res[counter] = {"copy_kib": kib_copy, "factor": factor,
+                            "kernels_kib": kern,
+                            "kernels_bytes": {nm: v * 1024.0 * factor for nm, v in kern.items()}}
+        names = sorted(res["FETCH_SIZE"]["kernels_bytes"])
+        per_kernel = {nm: round(res["FETCH_SIZE"]["kernels_bytes"][nm] +
+                                res["WRITE_SIZE"]["kernels_bytes"].get(nm, 0.0))
+                      for nm in names}
+        return {
+            "per_kernel_bytes": per_kernel,
+            "fetch_factor": round(res["FETCH_SIZE"]["factor"], 4),
+            "write_factor": round(res["WRITE_SIZE"]["factor"], 4),
+            "copy_fetch_kib": res["FETCH_SIZE"]["copy_kib"],
+            "copy_write_kib": res["WRITE_SIZE"]["copy_kib"],
+        }
+    finally:
+        shutil.rmtree(workdir, ignore_errors=True)
 
 
 def cpu_baseline(raw, n, k, x32):
@@ -121,7 +232,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--gemm-steps", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true")
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.pmc_child:
+        pmc_child()
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",
               file=sys.stderr)
@@ -133,8 +249,8 @@ def main():
     import jevons_qmm as jq
     from jevons_qmm import synth
 
-    n, k = 15360, 3840
-    ms = (1, 4, 8)
+    n, k = GEMV_N, GEMV_K
+    ms = GEMV_MS
     gpu = jq.Gpu(0)
     log("device", gpu.info.arch.decode(), "CUs", gpu.info.compute_units)
     raw = synth.weights(jq.Q4K, 2, n, k)
@@ -169,7 +285,8 @@ def main():
 
     # per-kernel durations (M = 1, 4, 8)
     reps = 100
-    kt = kernel_times_ms([lambda r, m=m: jq.matmul(gpu, xs[m], m, mats[r % copies], outs[m]) for m in ms], reps)
+    kt = [kernel_time_ms(lambda r, m=m: jq.matmul(gpu, xs[m], m, mats[r % copies], outs[m]), reps)
+          for m in ms]
     per_m = {m: {"kernel_us": round(t * 1e3, 3), "weight_GBps": round(wbytes / (t * 1e-3) / 1e9, 1)}
              for m, t in zip(ms, kt)}
     avg_kernel_ms = sum(kt) / len(kt)
@@ -197,7 +314,7 @@ def main():
     t3 = time.perf_counter()
     gemm_ms = (t3 - t2) * 1e3 / args.gemm_steps
     flops = 2.0 * mg * n * k
-    gk = kernel_times_ms([lambda r: gemm_step(r)], 30)[0]
+    gk = kernel_time_ms(gemm_step, 30)
     gemm = {
         "workload": f"Q4_K prefill GEMM M={mg} K={k} N={n}, bf16 activations (1% outlier columns x20), f32 out",
         "plan": {"bm": plan.bm, "bn": plan.bn, "splits": plan.splits},
@@ -214,6 +331,18 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline(raw, n, k, x8)
     if cpu:
         log("cpu:", cpu)
+
+    traffic, traffic_detail = None, None
+    if not args.no_traffic:
+        try:
+            traffic_detail = measure_traffic(wbytes)
+            gemv_bytes = [b for nm, b in traffic_detail["per_kernel_bytes"].items() if "qmv" in nm]
+            if gemv_bytes:
+                traffic = round(statistics.mean(gemv_bytes))
+            log("traffic:", traffic_detail)
+        except Exception as e:  # the counters are a report, not the measurement
+            traffic_detail = {"error": str(e)[:300]}
+            log("traffic measurement failed:", e)
 
     line = {
         "metric": METRIC,
@@ -240,8 +369,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
         },
+        "traffic_detail": traffic_detail,
         "gemm": gemm,
         "cpu_baseline": cpu,
     }

@@ -341,12 +341,16 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
     if (!x || !out) return fail(JV_ERR_INVALID, "null activation or output buffer");
     if (((uintptr_t)x & 15u) != 0) return fail(JV_ERR_INVALID, "activations must be 16-byte aligned");
 
-    if (plan.bm == 0 && w->fmt == JV_FMT_Q4K && m <= 16 && getenv("JV_QMV2") &&
+    // Small-row Q4_K kernels. Both sum a row's blocks in an order that does not depend on m,
+    // so every m takes the same kernel. The persistent kernel below is the default; JV_QMV2=WxP
+    // selects the per-tile kernel (W waves, P blocks in flight per wave), which is faster at
+    // m = 1 and slower from m = 4 on, where its per-tile activation staging costs occupancy.
+    const char *qmv2_env = getenv("JV_QMV2");
+    if (plan.bm == 0 && w->fmt == JV_FMT_Q4K && qmv2_env && m <= 16 &&
         w->n * w->experts * w->k / 2 < (1ull << 32)) {
-        // Small-row Q4_K kernel, one workgroup per 16-row tile.
-        int waves = 4, pf = 4;
-        sscanf(getenv("JV_QMV2"), "%dx%d", &waves, &pf);
-        if (!((waves == 4 && pf == 4) || (waves == 8 && pf == 2))) { waves = 4; pf = 4; }
+        int waves = 8, pf = 2;
+        if (qmv2_env) sscanf(qmv2_env, "%dx%d", &waves, &pf);
+        if (!((waves == 4 && pf == 4) || (waves == 8 && pf == 2))) { waves = 8; pf = 2; }
         const int U = (int)(w->k / 256);
         const int umax = (U + waves - 1) / waves;
         const int refill = umax > pf ? 1 : 0;

@@ -53,6 +53,41 @@ def test_device_decode_is_bit_exact(gpu, name, type_id):
     assert np.array_equal(part.view(np.uint32), want[37:87].view(np.uint32))
 
 
+def _kats():
+    import json
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_kats.json")
+    return json.load(open(path))
+
+
+def test_reference_kats_through_the_device_decoder(gpu):
+    """The reference's own known answers (quant.rs:199-226), decoded on the device: each KAT
+    block is row 0, block 0 of a zero 64 x K matrix."""
+    kats = _kats()
+    for name, type_id, block, bsize in (("q8_0", jq.Q8_0, 32, 34), ("q5_0", jq.Q5_0, 32, 22)):
+        n, k = 64, 64
+        raw = np.zeros(n * k // block * bsize, np.uint8)
+        raw[:bsize] = np.frombuffer(bytes.fromhex(kats[name]["block_hex"]), np.uint8)
+        w = jq.QMatrix.upload(gpu, type_id, n, k, 1, raw)
+        got = jq.dequant_rows(gpu, w, 0, 1).cpu().numpy()[0]
+        for i, v in kats[name]["expect"].items():
+            assert got[int(i)] == v, (name, i, got[int(i)])
+    # Q4_K: d = dmin = 1, every nibble 1, the KAT's scale bytes: element 32j decodes to s_j - m_j
+    kat = kats["q4k_scale_min"]
+    n, k = 64, 256
+    raw = np.zeros(n * 144, np.uint8)
+    raw[0:2] = np.frombuffer(np.array([1.0], np.float16).tobytes(), np.uint8)
+    raw[2:4] = raw[0:2]
+    raw[4:16] = kat["scale_bytes"]
+    raw[16:144] = 0x11
+    w = jq.QMatrix.upload(gpu, jq.Q4K, n, k, 1, raw)
+    got = jq.dequant_rows(gpu, w, 0, 1).cpu().numpy()[0]
+    for j, (sc, mn) in kat["pairs"].items():
+        for e in (0, 31):
+            assert got[32 * int(j) + e] == float(sc - mn), (j, e, got[32 * int(j) + e])
+
+
 def test_decode_of_reference_recipes_is_bit_exact(gpu):
     # Q8_0 weights of gpu/tests.rs:431-436 and the Q6_K table of :546-554
     rng = O.Rng(11)

@@ -6,6 +6,8 @@ library routine where one exists (numpy/torch float conversions, numpy matmul), 
 hand-built blocks whose decoded values follow from the block layout alone, so that a wrong
 index, shift, sign or dropped term fails one of them.
 """
+import json
+import os
 import struct
 
 import numpy as np
@@ -74,52 +76,49 @@ def test_type_table_matches_gguf_block_sizes(oracle):
 
 
 # ---------------------------------------------------------------- reference KATs
+# Vectors of the reference's own unit tests, kept in tests/golden/reference_kats.json
+# (written by tests/golden/make_kats.py).
+
+KATS = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                   "reference_kats.json")))
+
 
 def test_q4k_decodes_scale_high_bits_for_upper_groups(oracle):
-    # quant.rs:199-208
-    q = bytes([0xc1, 0x82, 0x43, 0x04, 0x85, 0xc6, 0x07, 0x48, 0x12, 0x34, 0x56, 0x78])
-    pairs = [oracle.q4k_scale_min(j, q) for j in range(8)]
-    assert pairs[0] == (1, 5)
-    assert pairs[4] == (50, 33)
-    assert pairs[7] == (8, 23)
+    kat = KATS["q4k_scale_min"]  # quant.rs:199-208
+    q = bytes(kat["scale_bytes"])
+    for j, pair in kat["pairs"].items():
+        assert oracle.q4k_scale_min(int(j), q) == tuple(pair)
 
 
 def test_q8_0_and_q5_0_dequantize_signed_values(oracle):
-    # quant.rs:210-226
-    q8 = bytearray(34)
-    q8[0:2] = f16_bytes(0.5)
-    q8[2] = (-4) & 0xFF
-    q8[33] = 7
-    out = oracle.dequantize(oracle.Q8_0, np.frombuffer(bytes(q8), np.uint8))
-    assert (out[0], out[31]) == (-2.0, 3.5)
-
-    q5 = bytearray(22)
-    q5[0:2] = f16_bytes(1.0)
-    q5[2:6] = struct.pack("<I", 1 | (1 << 16))
-    q5[6] = 0x3F
-    out = oracle.dequantize(oracle.Q5_0, np.frombuffer(bytes(q5), np.uint8))
-    assert (out[0], out[16], out[1]) == (15.0, 3.0, -16.0)
+    for name, type_id in (("q8_0", oracle.Q8_0), ("q5_0", oracle.Q5_0)):  # quant.rs:210-226
+        kat = KATS[name]
+        out = oracle.dequantize(type_id, np.frombuffer(bytes.fromhex(kat["block_hex"]), np.uint8))
+        for i, v in kat["expect"].items():
+            assert out[int(i)] == v, (name, i)
 
 
 def test_packing_splits_quants_and_scales_without_changing_values(oracle):
-    # quant.rs:228-237
-    q8 = bytearray(34)
-    q8[0:2] = f16_bytes(0.5)
-    q8[2:6] = bytes([1, 2, 3, 4])
-    q, h, s, d = oracle.pack(oracle.Q8_0, np.frombuffer(bytes(q8), np.uint8))
-    assert len(q) == 8 and list(d) == [0.5]
-    assert q[0] == struct.unpack("<I", bytes([1, 2, 3, 4]))[0]
+    kat = KATS["pack_q8_0"]  # quant.rs:228-237
+    q8 = bytes.fromhex(kat["block_hex"])
+    q, h, s, d = oracle.pack(oracle.Q8_0, np.frombuffer(q8, np.uint8))
+    assert len(q) == kat["q_words"] and list(d) == kat["d"]
+    assert q[0] == kat["q0"]
     with pytest.raises(oracle.OracleError):
-        oracle.pack(oracle.Q8_0, np.frombuffer(bytes(q8[:33]), np.uint8))
+        oracle.pack(oracle.Q8_0, np.frombuffer(q8[:33], np.uint8))
 
 
 def test_greedy_takes_the_first_argmax_with_its_stable_probability(oracle):
-    # crates/jevons-core/src/model.rs:221-234
-    tok, conf = oracle.greedy(np.array([1000.0, 1000.0 + np.log(np.float32(2.0)), 0.0], np.float32))
-    assert tok == 1 and abs(conf - 2.0 / 3.0) < 1e-4
-    assert oracle.greedy(np.array([3.0, 3.0], np.float32))[0] == 0
-    with pytest.raises(oracle.OracleError):
-        oracle.greedy(np.array([np.inf], np.float32))
+    for case in KATS["greedy"]["cases"]:  # crates/jevons-core/src/model.rs:221-234
+        logits = np.array([float(v) for v in case["logits"]], np.float32)
+        if case.get("error"):
+            with pytest.raises(oracle.OracleError):
+                oracle.greedy(logits)
+            continue
+        tok, conf = oracle.greedy(logits)
+        assert tok == case["index"]
+        if "prob" in case:
+            assert abs(conf - case["prob"]) < case["prob_tol"]
     with pytest.raises(oracle.OracleError):
         oracle.greedy(np.array([], np.float32))
     with pytest.raises(oracle.OracleError):
