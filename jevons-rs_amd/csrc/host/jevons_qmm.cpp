@@ -139,6 +139,8 @@ struct jv_ctx {
     hipModule_t module = nullptr;
     std::unordered_map<std::string, hipFunction_t> fns;
     jv_device_info info{};
+    void *pack = nullptr;  // packed activation fragments of the 256-row Q4_K product (grows)
+    size_t pack_bytes = 0;
 };
 
 struct jv_qmatrix {
@@ -405,6 +407,43 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
             return launch(ctx, name, dim3((unsigned)grid), dim3((unsigned)(64 * waves)), lds, stream, args);
         }
     }
+    if (plan.bm == 256) {
+        // Activations -> packed FP16 fragments, then the 256 x 128 Q4_K product.
+        const int mtiles = (int)((m + 255) / 256) * 16;
+        const size_t need = (size_t)mtiles * 16 * w->k * 2;
+        if (ctx->pack_bytes < need) {
+            if (ctx->pack) JV_HIP(hipFree(ctx->pack));
+            ctx->pack = nullptr;
+            ctx->pack_bytes = 0;
+            JV_HIP(hipMalloc(&ctx->pack, need));
+            ctx->pack_bytes = need;
+        }
+        PackXParams pk{};
+        pk.x = x;
+        pk.out = (uint16_t *)ctx->pack;
+        pk.M = (int32_t)m;
+        pk.K = (int32_t)w->k;
+        pk.ldx = (int32_t)w->k;
+        pk.act = (int32_t)act;
+        pk.mtiles = mtiles;
+        const int64_t threads = (int64_t)mtiles * (int64_t)(w->k / 32) * 64;
+        void *pargs[] = {&pk};
+        st = launch(ctx, "jv_pack_x", dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, pargs);
+        if (st != JV_OK) return st;
+        GemmParams gp{};
+        gp.xa = (const uint16_t *)ctx->pack;
+        gp.wq = w->q;
+        gp.out = out;
+        gp.M = (int32_t)m;
+        gp.N = (int32_t)w->n;
+        gp.K = (int32_t)w->k;
+        gp.ldo = (int32_t)w->n;
+        gp.out_type = (int32_t)out_type;
+        gp.mtiles = mtiles;
+        void *gargs[] = {&gp};
+        return launch(ctx, "jv_gemm_q4k_256x128", dim3((unsigned)(w->n / 128), (unsigned)(mtiles / 16)),
+                      dim3(512), 2 * 48 * 1024, stream, gargs);
+    }
     const int MT = plan_mt(plan), NT = plan_nt(plan);
     const int KU = fmt_unit(w->fmt);
     const int splits = (int)plan.splits;
@@ -539,6 +578,7 @@ jv_status jv_open(int device, jv_ctx **out) {
 void jv_close(jv_ctx *ctx) {
     if (!ctx) return;
     hipSetDevice(ctx->device);
+    if (ctx->pack) hipFree(ctx->pack);
     if (ctx->module) hipModuleUnload(ctx->module);
     delete ctx;
 }
@@ -711,8 +751,12 @@ jv_plan jv_plan_heuristic(const jv_qmatrix *w, size_t m, int row_invariant, size
 jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
     if (!w) return jv_plan{0, 0, 0};
     if (m <= 16) return jv_plan{0, 64, 1};
-    const uint32_t bm = m <= 32 ? 32 : (m <= 64 ? 64 : 128);
     const size_t cus = w->ctx ? (size_t)std::max(1, w->ctx->info.compute_units) : 256;
+    // Q4_K with enough rows for one 256 x 128 workgroup per compute unit (or nearly)
+    if (w->fmt == JV_FMT_Q4K && w->n % 128 == 0 && m >= 256 &&
+        ((m + 255) / 256) * (w->n / 128) * 16 >= cus * 15)
+        return jv_plan{256, 128, 1};
+    const uint32_t bm = m <= 32 ? 32 : (m <= 64 ? 64 : 128);
     const size_t mtiles = (m + bm - 1) / bm;
     uint32_t bn = 64;
     for (uint32_t c : {256u, 128u}) {
@@ -734,6 +778,9 @@ jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
 int jv_plan_valid(const jv_qmatrix *w, size_t m, jv_plan p) {
     if (!w) return 0;
     if (p.bm == 0) return m <= 16 && p.splits == 1;
+    // gfx950 Q4_K tile: 256 rows x 128 columns, whole K (no split)
+    if (p.bm == 256)
+        return w->fmt == JV_FMT_Q4K && p.bn == 128 && p.splits == 1 && w->n % 128 == 0;
     const bool bm_ok = p.bm == 32 || p.bm == 64 || p.bm == 128;
     const bool bn_ok = p.bn == 64 || p.bn == 128 || p.bn == 256;
     return bm_ok && bn_ok && w->n % p.bn == 0 && p.splits >= 1 && p.splits <= 16 &&

@@ -34,6 +34,8 @@
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// Plain vector (not HIP's uint4 struct): arrays of it stay in registers.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -64,10 +66,19 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
     return (x + 0x7fffu + ((x >> 16) & 1u)) >> 16;
 }
 
+// FP32 -> FP16, round to nearest even, of a value already rounded to FP32. The empty asm keeps
+// the compiler from fusing a preceding fma into v_fma_mix{lo,hi}_f16, which rounds the exact
+// product-sum to FP16 once; quant.rs rounds to FP32 first, and the two differ on ties. It is not
+// volatile: a volatile asm would also end the instruction scheduler's region at every element.
+__device__ __forceinline__ _Float16 f32_to_f16(float v) {
+    asm("" : "+v"(v));
+    return (_Float16)v;
+}
+
 __device__ __forceinline__ f16x8 pack8(const float v[8]) {
     f16x8 r;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = (_Float16)v[e];
+    for (int e = 0; e < 8; ++e) r[e] = f32_to_f16(v[e]);
     return r;
 }
 
@@ -607,9 +618,10 @@ struct Q4KItem {
 __device__ __forceinline__ void q4k_item_load(Q4KItem &it, const uint8_t *wq, int K, int tile,
                                               int u, int g, int r) {
     const uint8_t *tb = wq + ((size_t)tile * (size_t)(K / 256) + (size_t)u) * 2304u;
-    it.q0 = ld16(tb + (16 * g + r) * 16);
-    it.q1 = ld16(tb + 1024 + (16 * g + r) * 16);
-    it.hv = *(const uint32_t *)(tb + 2048 + r * 16 + 4 * g);
+    const uint32_t lq = (uint32_t)(16 * g + r) * 16u, lh = 2048u + (uint32_t)(r * 16 + 4 * g);
+    it.q0 = ld16(tb + lq);
+    it.q1 = ld16(tb + 1024u + lq);
+    it.hv = *(const uint32_t *)(tb + lh);
 }
 
 // All four head dwords of row r in every lane group, from lane 16g + r holding dword g.
@@ -654,7 +666,7 @@ __device__ __forceinline__ void q4k_block_v6(const Q4KItem &cur, const _Float16 
     // The magic held in a register lets each operand word be one v_and_or_b32 (a VOP3 op
     // cannot encode two 32-bit literals on this architecture).
     uint32_t magic = 0x64006400u;
-    asm volatile("" : "+v"(magic));
+    asm("" : "+v"(magic));
     // All eight sub-block products are independent: issue every MFMA into its own result
     // registers first and scale afterwards, so the matrix unit runs them back to back.
     f32x4 S[8];
@@ -1031,6 +1043,254 @@ extern "C" __global__ __launch_bounds__(256) void jv_reduce_splits(const float *
         ((float *)out)[i] = sum;
     else
         ((uint16_t *)out)[i] = (uint16_t)f2bf(sum);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Activation packing: rows -> FP16 MFMA A fragments (layout in qmm_params.h, PackXParams).
+// Conversions equal the staging of the tiled kernel: FP16 as is, BF16 and FP32 rounded to nearest
+// even. One thread per (fragment, lane).
+// ---------------------------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(256) void jv_pack_x(PackXParams p) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;  // fragment * 64 + lane
+    const int U = p.K >> 8;
+    if (t >= (int64_t)p.mtiles * U * 8 * 64) return;
+    const int lane = (int)(t & 63);
+    const int64_t f = t >> 6;
+    const int s = (int)(f & 7);
+    const int64_t mu = f >> 3;
+    const int u = (int)(mu % U);
+    const int mt = (int)(mu / U);
+    const int row = mt * 16 + (lane & 15);
+    const int col = u * 256 + s * 32 + (lane >> 4) * 8;
+    f16x8 h;
+    if (row < p.M) {
+        const size_t o = (size_t)row * (size_t)p.ldx + (size_t)col;
+        if (p.act == 0) {
+            h = __builtin_bit_cast(f16x8, *(const uint4 *)((const uint16_t *)p.x + o));
+        } else if (p.act == 1) {
+            const uint4 w = *(const uint4 *)((const uint16_t *)p.x + o);
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                h[2 * e] = (_Float16)bf2f(ww[e]);
+                h[2 * e + 1] = (_Float16)bf2f(ww[e] >> 16);
+            }
+        } else {
+            const float4 a = *(const float4 *)((const float *)p.x + o);
+            const float4 b = *(const float4 *)((const float *)p.x + o + 4);
+            h[0] = (_Float16)a.x; h[1] = (_Float16)a.y; h[2] = (_Float16)a.z; h[3] = (_Float16)a.w;
+            h[4] = (_Float16)b.x; h[5] = (_Float16)b.y; h[6] = (_Float16)b.z; h[7] = (_Float16)b.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = (_Float16)0.f;
+    }
+    *(f16x8 *)(p.out + t * 8) = h;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Q4_K tiled product, 256 x 128 output tile per workgroup of 8 waves (two per SIMD, so one
+// wave's weight decode and LDS traffic overlap the other's MFMAs).
+//
+// Wave w computes rows [64 (w >> 1), +64) x columns [64 (w & 1), +64) of the tile: 4 x 4 MFMA
+// 16x16x32 accumulators. K advances in stages of 64 (two 32-k steps; four stages per Q4_K
+// block), double-buffered in LDS:
+//   A: 16 m-tiles x 2 steps of packed activation fragments (32 KB), copied from jv_pack_x's
+//      output, each wave moving 4 of them;
+//   B: 8 weight tiles x 2 steps of FP16 weight fragments (16 KB). Wave w decodes weight tile w
+//      (rows 16w .. 16w + 15 of the tile) exactly as quant.rs does (FP32 decode, one RNE
+//      rounding to FP16; gemm.rs:131-284's tile format), so every weight is decoded once per
+//      workgroup and read by the four waves that share its columns.
+// Fragments sit in LDS in lane order (1 KB each), so every LDS access is one contiguous
+// 16-byte-per-lane read or write. Each output element is the same MFMA chain over K as in the
+// other tiled kernels (32-k steps in order, lane group g holding k 32s + 8g .. +8), so the
+// result is bitwise identical to theirs.
+//
+// Loads are ordered so that waiting for one stage's activations never waits for weights: the
+// activation fragments of stage t + 2 are issued during stage t, the weights of block b + 1 at
+// the start of block b, after them.
+// ---------------------------------------------------------------------------------------------
+namespace {
+
+constexpr int kGemmStageBytes = 48 * 1024;  // A 32 KB + B 16 KB
+
+// All 8 (d s_j, dmin m_j) of row r of a block, from the lane's head dword (see q4k_item_load):
+// lane group g decodes sub-blocks 2g, 2g + 1, and permlane swaps share them.
+__device__ __forceinline__ void q4k_row_scales(uint32_t hv, int g, float dsc[8], float dmm[8]) {
+    const uint4 hd = q4k_head_gather(hv);
+    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+    uint32_t sc[2], mn[2];
+    q4k_pair_scales(hd, g, sc, mn);
+    const uint4 a0 = q4k_head_gather(__builtin_bit_cast(uint32_t, d * (float)sc[0]));
+    const uint4 a1 = q4k_head_gather(__builtin_bit_cast(uint32_t, d * (float)sc[1]));
+    const uint4 b0 = q4k_head_gather(__builtin_bit_cast(uint32_t, dmin * (float)mn[0]));
+    const uint4 b1 = q4k_head_gather(__builtin_bit_cast(uint32_t, dmin * (float)mn[1]));
+    const uint32_t A0[4] = {a0.x, a0.y, a0.z, a0.w}, A1[4] = {a1.x, a1.y, a1.z, a1.w};
+    const uint32_t B0[4] = {b0.x, b0.y, b0.z, b0.w}, B1[4] = {b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        dsc[2 * k] = __builtin_bit_cast(float, A0[k]);
+        dsc[2 * k + 1] = __builtin_bit_cast(float, A1[k]);
+        dmm[2 * k] = __builtin_bit_cast(float, B0[k]);
+        dmm[2 * k + 1] = __builtin_bit_cast(float, B1[k]);
+    }
+}
+
+// FP16 fragments of sub-blocks 2pr (low nibbles) and 2pr + 1 (high nibbles) for lane group g:
+// elements 8g .. 8g + 7 of each, decoded as quant.rs:25-41 does.
+__device__ __forceinline__ void q4k_pair_frags(const Q4KItem &it, int pr, const float dsc[8],
+                                               const float dmm[8], f16x8 &lo, f16x8 &hi) {
+    const uint32_t w0 = pr == 0 ? it.q0.x : pr == 1 ? it.q0.z : pr == 2 ? it.q1.x : it.q1.z;
+    const uint32_t w1 = pr == 0 ? it.q0.y : pr == 1 ? it.q0.w : pr == 2 ? it.q1.y : it.q1.w;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int j = 2 * pr + h;
+        const uint32_t n0 = h ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
+        const uint32_t n1 = h ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
+        // stored byte order {0, 2, 1, 3}: byte 1 holds element 2, byte 2 element 1
+        const float q[8] = {(float)(uint8_t)n0, (float)(uint8_t)(n0 >> 16), (float)(uint8_t)(n0 >> 8),
+                            (float)(uint8_t)(n0 >> 24), (float)(uint8_t)n1, (float)(uint8_t)(n1 >> 16),
+                            (float)(uint8_t)(n1 >> 8), (float)(uint8_t)(n1 >> 24)};
+        f16x8 v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = f32_to_f16(__builtin_fmaf(q[e], dsc[j], -dmm[j]));
+        if (h == 0)
+            lo = v;
+        else
+            hi = v;
+    }
+}
+
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(512) void jv_gemm_q4k_256x128(GemmParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, r = lane & 15;
+    const int mq = w >> 1, nh = w & 1;
+    const int U = p.K >> 8;
+    const int mt0 = blockIdx.y * 16;  // first 16-row activation tile
+    const int t0 = blockIdx.x * 8;    // first 16-row weight tile
+    const int stages = 4 * U;
+    const uint32_t lo16 = (uint32_t)lane * 16u;  // this lane's bytes in a 1 KB fragment
+
+    // Activation fragments: wave w copies fragments 4w .. 4w + 3 of a stage, (m-tile, step) =
+    // (f >> 1, f & 1): m-tiles 2w and 2w + 1, both steps. Fragment (mt, st, ss) of the packed
+    // activations starts at fragment ((mt0 + mt) U + st / 4) 8 + 2 (st % 4) + ss.
+    const uint8_t *xa = (const uint8_t *)p.xa;
+    auto load_a = [&](u32x4 *dst, int st) __attribute__((always_inline)) {
+        st = min(st, stages - 1);
+        const int u = st >> 2, s0 = 2 * (st & 3);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const size_t frag = ((size_t)(mt0 + 2 * w + j) * (size_t)U + (size_t)u) * 8 + (size_t)s0;
+            const uint8_t *src = xa + frag * 1024;  // uniform
+            dst[2 * j] = *(const u32x4 *)(src + lo16);
+            dst[2 * j + 1] = *(const u32x4 *)(src + 1024 + lo16);
+        }
+    };
+    auto store_a = [&](const u32x4 *src, int buf) __attribute__((always_inline)) {
+        uint8_t *base = smem + buf * kGemmStageBytes + (4 * w) * 1024 + lo16;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *(u32x4 *)(base + j * 1024) = src[j];
+    };
+    auto load_w = [&](Q4KItem &dst, int u) __attribute__((always_inline)) {
+        q4k_item_load(dst, p.wq, p.K, t0 + w, min(u, U - 1), g, r);
+    };
+    float dsc[8], dmm[8];
+    auto decode_b = [&](const Q4KItem &it, int pr, int buf) __attribute__((always_inline)) {
+        uint8_t *base = smem + buf * kGemmStageBytes + 32 * 1024 + lo16;
+        f16x8 lo, hi;
+        q4k_pair_frags(it, pr, dsc, dmm, lo, hi);
+        *(f16x8 *)(base + (w * 2 + 0) * 1024) = lo;
+        *(f16x8 *)(base + (w * 2 + 1) * 1024) = hi;
+    };
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto mfma_stage = [&](int buf) __attribute__((always_inline)) {
+        const uint8_t *base = smem + buf * kGemmStageBytes + lo16;
+        // all 16 fragments of the stage first, so the reads of step 1 overlap step 0's MFMAs
+        f16x8 bf[2][4], af[2][4];
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss) {
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt)
+                bf[ss][nt] = *(const f16x8 *)(base + 32 * 1024 + ((4 * nh + nt) * 2 + ss) * 1024);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+                af[ss][mt] = *(const f16x8 *)(base + ((4 * mq + mt) * 2 + ss) * 1024);
+        }
+#pragma unroll
+        for (int ss = 0; ss < 2; ++ss)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[ss][mt], bf[ss][nt], acc[mt][nt], 0, 0, 0);
+    };
+
+    // prologue: stage 0 in buffer 0; activations of stage 1 and weights of block 1 in flight
+    Q4KItem cur, nxt;
+    u32x4 ra[4], rb[4];  // activation fragments of odd / even stages in flight
+    load_a(rb, 0);
+    load_w(cur, 0);
+    load_a(ra, 1);
+    load_w(nxt, 1);
+    store_a(rb, 0);
+    q4k_row_scales(cur.hv, g, dsc, dmm);
+    decode_b(cur, 0, 0);
+    lds_barrier();
+
+    // One step of the stage pipeline: MFMAs of stage st from buffer st & 1; stage st + 1 (its
+    // activations in `next`, issued a stage ago) decoded and stored into the other buffer;
+    // activations of stage st + 2 issued into `fresh`.
+    auto step = [&](int st, int pr, u32x4 *next, u32x4 *fresh) __attribute__((always_inline)) {
+        load_a(fresh, st + 2);
+        mfma_stage(pr & 1);
+        if (st + 1 < stages) {
+            if (pr == 3) {  // the next stage starts a block: its raw weights are in nxt
+                cur = nxt;
+                load_w(nxt, (st >> 2) + 2);
+                q4k_row_scales(cur.hv, g, dsc, dmm);
+            }
+            decode_b(cur, (pr + 1) & 3, (pr & 1) ^ 1);
+            store_a(next, (pr & 1) ^ 1);
+        }
+        lds_barrier();
+    };
+    for (int b = 0; b < U; ++b) {
+        step(4 * b + 0, 0, ra, rb);
+        step(4 * b + 1, 1, rb, ra);
+        step(4 * b + 2, 2, ra, rb);
+        step(4 * b + 3, 3, rb, ra);
+    }
+
+    // epilogue: lane (g, r) holds column r, rows 4g .. 4g + 3 of each 16 x 16 tile
+    const bool f32_out = p.out_type == 0;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+            const int col = (t0 + 4 * nh + nt) * 16 + r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = (mt0 + 4 * mq + mt) * 16 + 4 * g + i;
+                if (m < p.M) {
+                    const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
+                    if (f32_out)
+                        ((float *)p.out)[o] = acc[mt][nt][i];
+                    else
+                        ((uint16_t *)p.out)[o] = (uint16_t)f2bf(acc[mt][nt][i]);
+                }
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------

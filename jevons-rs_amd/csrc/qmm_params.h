@@ -32,6 +32,24 @@ struct DequantParams {
     int32_t f16_out;     // 0: FP32 values, 1: FP16 tile values
 };
 
+// Activation rows -> FP16 MFMA A fragments of 1 KB: fragment (mt * U + u) * 8 + s (U = K / 256)
+// holds, for lane 16g + r, x[16 mt + r][256 u + 32 s + 8 g + e], e < 8; rows >= M are zero.
+struct PackXParams {
+    const void *x;       // [M][ldx] of `act`
+    uint16_t *out;       // FP16 bits, mtiles * (K / 32) fragments of 512 elements
+    int32_t M, K, ldx, act;
+    int32_t mtiles;      // 16-row tiles packed (M rounded up to the product's row tile)
+};
+
+// Q4_K tiled product over packed activation fragments (jv_pack_x output).
+struct GemmParams {
+    const uint16_t *xa;  // packed activations
+    const uint8_t *wq;   // Q4_K tile layout
+    void *out;           // [M][ldo] of `out_type`
+    int32_t M, N, K, ldo, out_type;
+    int32_t mtiles;
+};
+
 // GGML blocks (device copy of the upload) -> device layout.
 struct RepackParams {
     const uint8_t *raw;

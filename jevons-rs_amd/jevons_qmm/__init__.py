@@ -217,6 +217,8 @@ class Plan:
     ROW_TILES = (32, 64, 128)
     COL_TILES = (64, 128)
     GFX950_COL_TILES = (64, 128, 256)
+    # gfx950 Q4_K tile: Plan(256, 128, 1)
+    GFX950_Q4K_TILE = (256, 128)
 
     def __init__(self, bm: int, bn: int, splits: int):
         self.bm, self.bn, self.splits = bm, bn, splits

@@ -117,6 +117,7 @@ def all_plans(w, m):
         for bn in jq.Plan.GFX950_COL_TILES:
             for splits in (1, 2, 8):
                 plans.append(jq.Plan(bm, bn, splits))
+    plans.append(jq.Plan(256, 128, 1))  # gfx950 Q4_K tile
     return [p for p in plans if p.valid_for(w, m)]
 
 
@@ -180,6 +181,28 @@ def test_reference_dense_plan_recipe(gpu):
                     reference = got
                 else:
                     assert np.array_equal(reference, got), (m, plan)
+
+
+@pytest.mark.parametrize("name,type_id", FORMATS)
+def test_tiled_products_use_the_reference_f16_tile(gpu, name, type_id):
+    """Identity activations make every output one product 1 * w, so the tiled kernels' outputs
+    are their on-chip weight tile: it must equal the reference's f16 tile (the f32 decode of
+    quant.rs rounded to nearest even, gemm.rs:131-284) bit for bit."""
+    n, k = 128, 512
+    say("identity tile", name, n, k)
+    w, raw = make_matrix(gpu, type_id, n, k, seed=17)
+    tile = O.dequantize(type_id, raw).reshape(n, k).astype(np.float16).astype(np.float32)
+    x = torch.eye(k, dtype=torch.float16, device="cuda")
+    plans = [jq.Plan(32, 64, 1), jq.Plan(64, 128, 1), jq.Plan(128, 64, 1), jq.Plan(128, 128, 1),
+             jq.Plan(256, 128, 1)]
+    for plan in [pl for pl in plans if pl.valid_for(w, k)]:
+        out = torch.empty((k, n), dtype=torch.float32, device="cuda")
+        jq.matmul_plan(gpu, x, k, w, out, None, plan)
+        got = out.cpu().numpy()
+        want = tile.T.copy() + np.float32(0.0)  # a product's sum of one w and zeros turns -0 into +0
+        bad = np.argwhere(got.view(np.uint32) != want.view(np.uint32))
+        detail = [(int(i), int(j), float(got[i, j]), float(want[i, j])) for i, j in bad[:6]]
+        assert bad.size == 0, f"{name} {plan}: {len(bad)} elements differ, e.g. (k, n, got, tile) {detail}"
 
 
 def test_bf16_output_rounds_the_f32_result(gpu):
@@ -351,3 +374,8 @@ def test_plan_rules_follow_the_reference(gpu):
     assert not jq.Plan(0, 128, 2).valid_for(w, 4)
     assert jq.Plan(128, 128, 8).valid_for(w, 4) and not jq.Plan(128, 128, 9).valid_for(w, 4)
     assert not jq.Plan(128, 128, 0).valid_for(w, 4)
+    # the gfx950 256 x 128 tile exists for Q4_K only, without split-K
+    assert not jq.Plan(256, 128, 1).valid_for(w, 512)
+    w4 = jq.QMatrix.upload(gpu, jq.Q4K, 256, 512, 1, synth.weights(jq.Q4K, 1, 256, 512))
+    assert jq.Plan(256, 128, 1).valid_for(w4, 512)
+    assert not jq.Plan(256, 128, 2).valid_for(w4, 512) and not jq.Plan(256, 64, 1).valid_for(w4, 512)
