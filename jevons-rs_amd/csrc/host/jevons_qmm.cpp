@@ -426,7 +426,7 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         pk.ldx = (int32_t)w->k;
         pk.act = (int32_t)act;
         pk.mtiles = mtiles;
-        const int64_t threads = (int64_t)mtiles * (int64_t)(w->k / 32) * 64;
+        const int64_t threads = (int64_t)mtiles * (int64_t)(w->k / 256) * 2 * 64;
         void *pargs[] = {&pk};
         st = launch(ctx, "jv_pack_x", dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, pargs);
         if (st != JV_OK) return st;
@@ -439,10 +439,9 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         gp.K = (int32_t)w->k;
         gp.ldo = (int32_t)w->n;
         gp.out_type = (int32_t)out_type;
-        gp.mtiles = mtiles;
         void *gargs[] = {&gp};
         return launch(ctx, "jv_gemm_q4k_256x128", dim3((unsigned)(w->n / 128), (unsigned)(mtiles / 16)),
-                      dim3(512), 2 * 48 * 1024, stream, gargs);
+                      dim3(512), 4 * 24 * 1024, stream, gargs);
     }
     const int MT = plan_mt(plan), NT = plan_nt(plan);
     const int KU = fmt_unit(w->fmt);

@@ -1048,71 +1048,87 @@ extern "C" __global__ __launch_bounds__(256) void jv_reduce_splits(const float *
 // ---------------------------------------------------------------------------------------------
 // Activation packing: rows -> FP16 MFMA A fragments (layout in qmm_params.h, PackXParams).
 // Conversions equal the staging of the tiled kernel: FP16 as is, BF16 and FP32 rounded to nearest
-// even. One thread per (fragment, lane).
+// even. Thread ((mt * U + u) * 2 + half) * 64 + lane packs fragments s = 4 half .. 4 half + 3
+// of (mt, u), with four 16-byte loads in flight.
 // ---------------------------------------------------------------------------------------------
 extern "C" __global__ __launch_bounds__(256) void jv_pack_x(PackXParams p) {
-    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;  // fragment * 64 + lane
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int U = p.K >> 8;
-    if (t >= (int64_t)p.mtiles * U * 8 * 64) return;
+    if (t >= (int64_t)p.mtiles * U * 2 * 64) return;
     const int lane = (int)(t & 63);
-    const int64_t f = t >> 6;
-    const int s = (int)(f & 7);
-    const int64_t mu = f >> 3;
-    const int u = (int)(mu % U);
-    const int mt = (int)(mu / U);
-    const int row = mt * 16 + (lane & 15);
-    const int col = u * 256 + s * 32 + (lane >> 4) * 8;
-    f16x8 h;
+    const int64_t q = t >> 6;
+    const int half = (int)(q & 1);
+    const int64_t mu = q >> 1;
+    const int row = (int)(mu / U) * 16 + (lane & 15);
+    const int col0 = (int)(mu % U) * 256 + half * 128 + (lane >> 4) * 8;
+    uint16_t *dst = p.out + ((mu * 8 + 4 * half) * 64 + lane) * 8;
+    f16x8 h[4];
     if (row < p.M) {
-        const size_t o = (size_t)row * (size_t)p.ldx + (size_t)col;
+        const size_t o = (size_t)row * (size_t)p.ldx + (size_t)col0;
         if (p.act == 0) {
-            h = __builtin_bit_cast(f16x8, *(const uint4 *)((const uint16_t *)p.x + o));
-        } else if (p.act == 1) {
-            const uint4 w = *(const uint4 *)((const uint16_t *)p.x + o);
-            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+            uint4 w[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                h[2 * e] = (_Float16)bf2f(ww[e]);
-                h[2 * e + 1] = (_Float16)bf2f(ww[e] >> 16);
+            for (int s = 0; s < 4; ++s) w[s] = *(const uint4 *)((const uint16_t *)p.x + o + 32 * s);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) h[s] = __builtin_bit_cast(f16x8, w[s]);
+        } else if (p.act == 1) {
+            uint4 w[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) w[s] = *(const uint4 *)((const uint16_t *)p.x + o + 32 * s);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const uint32_t ww[4] = {w[s].x, w[s].y, w[s].z, w[s].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    h[s][2 * e] = (_Float16)bf2f(ww[e]);
+                    h[s][2 * e + 1] = (_Float16)bf2f(ww[e] >> 16);
+                }
             }
         } else {
-            const float4 a = *(const float4 *)((const float *)p.x + o);
-            const float4 b = *(const float4 *)((const float *)p.x + o + 4);
-            h[0] = (_Float16)a.x; h[1] = (_Float16)a.y; h[2] = (_Float16)a.z; h[3] = (_Float16)a.w;
-            h[4] = (_Float16)b.x; h[5] = (_Float16)b.y; h[6] = (_Float16)b.z; h[7] = (_Float16)b.w;
+            float4 a[4], b[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                a[s] = *(const float4 *)((const float *)p.x + o + 32 * s);
+                b[s] = *(const float4 *)((const float *)p.x + o + 32 * s + 4);
+            }
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                h[s][0] = (_Float16)a[s].x; h[s][1] = (_Float16)a[s].y; h[s][2] = (_Float16)a[s].z; h[s][3] = (_Float16)a[s].w;
+                h[s][4] = (_Float16)b[s].x; h[s][5] = (_Float16)b[s].y; h[s][6] = (_Float16)b[s].z; h[s][7] = (_Float16)b[s].w;
+            }
         }
     } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) h[e] = (_Float16)0.f;
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[s][e] = (_Float16)0.f;
     }
-    *(f16x8 *)(p.out + t * 8) = h;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) *(f16x8 *)(dst + s * 512) = h[s];
 }
 
 // ---------------------------------------------------------------------------------------------
-// Q4_K tiled product, 256 x 128 output tile per workgroup of 8 waves (two per SIMD, so one
-// wave's weight decode and LDS traffic overlap the other's MFMAs).
+// Q4_K tiled product, 256 x 128 output tile per workgroup of 8 waves (two per SIMD).
 //
-// Wave w computes rows [64 (w >> 1), +64) x columns [64 (w & 1), +64) of the tile: 4 x 4 MFMA
-// 16x16x32 accumulators. K advances in stages of 64 (two 32-k steps; four stages per Q4_K
-// block), double-buffered in LDS:
-//   A: 16 m-tiles x 2 steps of packed activation fragments (32 KB), copied from jv_pack_x's
-//      output, each wave moving 4 of them;
-//   B: 8 weight tiles x 2 steps of FP16 weight fragments (16 KB). Wave w decodes weight tile w
-//      (rows 16w .. 16w + 15 of the tile) exactly as quant.rs does (FP32 decode, one RNE
-//      rounding to FP16; gemm.rs:131-284's tile format), so every weight is decoded once per
-//      workgroup and read by the four waves that share its columns.
-// Fragments sit in LDS in lane order (1 KB each), so every LDS access is one contiguous
-// 16-byte-per-lane read or write. Each output element is the same MFMA chain over K as in the
-// other tiled kernels (32-k steps in order, lane group g holding k 32s + 8g .. +8), so the
-// result is bitwise identical to theirs.
+// Wave w = 2 mq + nh computes a 64 x 64 block of the tile: activation m-tiles 4 mq .. 4 mq + 3
+// and weight n-tiles 4 nh .. 4 nh + 3 (16 rows each), 4 x 4 MFMA 16x16x32 accumulators. K
+// advances in stages of 32 (one Q4_K sub-block), in four LDS buffers of 24 KB:
+//   A: the workgroup's 16 activation fragments of the stage (1 KB each, lane order), copied
+//      from jv_pack_x's output. Wave w copies m-tiles 4 mq + 2 nh, +1 (two of its own four);
+//   B: the 8 weight fragments, decoded from Q4_K exactly as quant.rs does (FP32 decode, one RNE
+//      rounding to FP16; gemm.rs:131-284's tile format). Wave w decodes n-tile 4 nh + mq (one
+//      of its own four), so every weight is decoded once per workgroup.
+// A wave takes the two activation and one weight fragment it wrote from its registers and
+// reads the other five from LDS; the reads for stage t + 1 are issued while stage t's MFMAs
+// run, and stage t + 2 is written meanwhile. Register slots are ordered own-first, so which
+// fragment is whose is fixed at compile time.
 //
-// Loads are ordered so that waiting for one stage's activations never waits for weights: the
-// activation fragments of stage t + 2 are issued during stage t, the weights of block b + 1 at
-// the start of block b, after them.
+// Each output element is the same MFMA chain over K as in the other tiled kernels (32-k steps
+// in order, lane group g holding k 32s + 8g .. +8), so the result is bitwise identical to theirs.
 // ---------------------------------------------------------------------------------------------
 namespace {
 
-constexpr int kGemmStageBytes = 48 * 1024;  // A 32 KB + B 16 KB
+constexpr int kGemmBufBytes = 24 * 1024;  // A 16 KB + B 8 KB
 
 // All 8 (d s_j, dmin m_j) of row r of a block, from the lane's head dword (see q4k_item_load):
 // lane group g decodes sub-blocks 2g, 2g + 1, and permlane swaps share them.
@@ -1136,162 +1152,204 @@ __device__ __forceinline__ void q4k_row_scales(uint32_t hv, int g, float dsc[8],
     }
 }
 
-// FP16 fragments of sub-blocks 2pr (low nibbles) and 2pr + 1 (high nibbles) for lane group g:
-// elements 8g .. 8g + 7 of each, decoded as quant.rs:25-41 does.
-__device__ __forceinline__ void q4k_pair_frags(const Q4KItem &it, int pr, const float dsc[8],
-                                               const float dmm[8], f16x8 &lo, f16x8 &hi) {
+// FP16 fragment of sub-block j for lane group g: elements 32j + 8g .. +7, decoded as
+// quant.rs:25-41 does (low nibbles of byte pair j / 2 for even j, high nibbles for odd j).
+__device__ __forceinline__ f16x8 q4k_sub_frag(const Q4KItem &it, int j, float dsc, float dmm) {
+    const int pr = j >> 1;
     const uint32_t w0 = pr == 0 ? it.q0.x : pr == 1 ? it.q0.z : pr == 2 ? it.q1.x : it.q1.z;
     const uint32_t w1 = pr == 0 ? it.q0.y : pr == 1 ? it.q0.w : pr == 2 ? it.q1.y : it.q1.w;
+    const uint32_t n0 = (j & 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
+    const uint32_t n1 = (j & 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
+    // stored byte order {0, 2, 1, 3}: byte 1 holds element 2, byte 2 element 1
+    const float q[8] = {(float)(uint8_t)n0, (float)(uint8_t)(n0 >> 16), (float)(uint8_t)(n0 >> 8),
+                        (float)(uint8_t)(n0 >> 24), (float)(uint8_t)n1, (float)(uint8_t)(n1 >> 16),
+                        (float)(uint8_t)(n1 >> 8), (float)(uint8_t)(n1 >> 24)};
+    f16x8 v;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int j = 2 * pr + h;
-        const uint32_t n0 = h ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
-        const uint32_t n1 = h ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
-        // stored byte order {0, 2, 1, 3}: byte 1 holds element 2, byte 2 element 1
-        const float q[8] = {(float)(uint8_t)n0, (float)(uint8_t)(n0 >> 16), (float)(uint8_t)(n0 >> 8),
-                            (float)(uint8_t)(n0 >> 24), (float)(uint8_t)n1, (float)(uint8_t)(n1 >> 16),
-                            (float)(uint8_t)(n1 >> 8), (float)(uint8_t)(n1 >> 24)};
-        f16x8 v;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = f32_to_f16(__builtin_fmaf(q[e], dsc[j], -dmm[j]));
-        if (h == 0)
-            lo = v;
-        else
-            hi = v;
-    }
+    for (int e = 0; e < 8; ++e) v[e] = f32_to_f16(__builtin_fmaf(q[e], dsc, -dmm));
+    return v;
 }
 
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(512) void jv_gemm_q4k_256x128(GemmParams p) {
+// WM x WN waves; wave w = WN mq + nh computes m-tiles MT mq .. +MT and n-tiles NT nh .. +NT
+// (MT = 16 / WM, NT = 8 / WN) of the 256 x 128 tile.
+template <int WM, int WN>
+__device__ __forceinline__ void gemm_q4k_body(const GemmParams &p) {
+    constexpr int W = WM * WN, MT = 16 / WM, NT = 8 / WN;
+    constexpr int AS = MT / WN;  // activation fragments a wave stages per stage (own m slots)
+    constexpr int BS = NT / WM;  // weight fragments a wave decodes per stage (own n slots)
+    static_assert(AS * W == 16 && BS * W == 8, "tile split");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, r = lane & 15;
-    const int mq = w >> 1, nh = w & 1;
+    const int mq = w / WN, nh = w % WN;
     const int U = p.K >> 8;
     const int mt0 = blockIdx.y * 16;  // first 16-row activation tile
     const int t0 = blockIdx.x * 8;    // first 16-row weight tile
-    const int stages = 4 * U;
+    const int stages = 8 * U;
     const uint32_t lo16 = (uint32_t)lane * 16u;  // this lane's bytes in a 1 KB fragment
 
-    // Activation fragments: wave w copies fragments 4w .. 4w + 3 of a stage, (m-tile, step) =
-    // (f >> 1, f & 1): m-tiles 2w and 2w + 1, both steps. Fragment (mt, st, ss) of the packed
-    // activations starts at fragment ((mt0 + mt) U + st / 4) 8 + 2 (st % 4) + ss.
-    const uint8_t *xa = (const uint8_t *)p.xa;
+    // Local m-tile of slot i: own slots first (the AS this wave stages), then the rest of the
+    // wave's MT in order; n-tile of slot k likewise with the BS tiles it decodes.
+    auto m_of = [&](int i) __attribute__((always_inline)) {
+        const int own0 = AS * nh;
+        return MT * mq + (i < AS ? own0 + i : ((own0 + i) % MT));
+    };
+    auto n_of = [&](int k) __attribute__((always_inline)) {
+        const int own0 = BS * mq;
+        return NT * nh + (k < BS ? own0 + k : ((own0 + k) % NT));
+    };
+
+    // The packed fragment of m-tile mt at stage st is fragment (mt U) 8 + st: consecutive
+    // stages of one m-tile are consecutive 1 KB fragments.
+    const uint8_t *xa_own[AS];
+#pragma unroll
+    for (int i = 0; i < AS; ++i)
+        xa_own[i] = (const uint8_t *)p.xa + (size_t)(mt0 + m_of(i)) * (size_t)U * 8192u + lo16;
     auto load_a = [&](u32x4 *dst, int st) __attribute__((always_inline)) {
-        st = min(st, stages - 1);
-        const int u = st >> 2, s0 = 2 * (st & 3);
+        const uint32_t off = (uint32_t)min(st, stages - 1) * 1024u;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const size_t frag = ((size_t)(mt0 + 2 * w + j) * (size_t)U + (size_t)u) * 8 + (size_t)s0;
-            const uint8_t *src = xa + frag * 1024;  // uniform
-            dst[2 * j] = *(const u32x4 *)(src + lo16);
-            dst[2 * j + 1] = *(const u32x4 *)(src + 1024 + lo16);
+        for (int i = 0; i < AS; ++i) dst[i] = *(const u32x4 *)(xa_own[i] + off);
+    };
+    // four LDS buffers, stage st in buffer st % 4 (a compile-time index in the unrolled loop)
+    auto buf_of = [&](int st) __attribute__((always_inline)) { return smem + (st & 3) * kGemmBufBytes + lo16; };
+    auto store_a = [&](const u32x4 *src, int st) __attribute__((always_inline)) {
+        uint8_t *base = buf_of(st);
+#pragma unroll
+        for (int i = 0; i < AS; ++i) *(u32x4 *)(base + m_of(i) * 1024) = src[i];
+    };
+    auto load_w = [&](Q4KItem *dst, int u) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < BS; ++k) q4k_item_load(dst[k], p.wq, p.K, t0 + n_of(k), min(u, U - 1), g, r);
+    };
+    float dsc[BS][8], dmm[BS][8];
+    auto block_scales = [&](const Q4KItem *it) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < BS; ++k) q4k_row_scales(it[k].hv, g, dsc[k], dmm[k]);
+    };
+    auto store_b = [&](const f16x8 *v, int st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < BS; ++k) *(f16x8 *)(buf_of(st) + 16 * 1024 + n_of(k) * 1024) = v[k];
+    };
+    // the fragments of stage st this wave does not hold
+    auto read_other = [&](f16x8 *fa, f16x8 *fb, int st) __attribute__((always_inline)) {
+        const uint8_t *base = buf_of(st);
+#pragma unroll
+        for (int i = 0; i < MT - AS; ++i) fa[i] = *(const f16x8 *)(base + m_of(AS + i) * 1024);
+#pragma unroll
+        for (int k = 0; k < NT - BS; ++k) fb[k] = *(const f16x8 *)(base + 16 * 1024 + n_of(BS + k) * 1024);
+    };
+
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int k = 0; k < NT; ++k) acc[i][k] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto mfma_stage = [&](const u32x4 *aown, const f16x8 *bown, const f16x8 *fa, const f16x8 *fb)
+        __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+            const f16x8 a = i < AS ? __builtin_bit_cast(f16x8, aown[i]) : fa[i - AS];
+#pragma unroll
+            for (int k = 0; k < NT; ++k)
+                acc[i][k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, k < BS ? bown[k] : fb[k - BS], acc[i][k], 0, 0, 0);
         }
     };
-    auto store_a = [&](const u32x4 *src, int buf) __attribute__((always_inline)) {
-        uint8_t *base = smem + buf * kGemmStageBytes + (4 * w) * 1024 + lo16;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) *(u32x4 *)(base + j * 1024) = src[j];
-    };
-    auto load_w = [&](Q4KItem &dst, int u) __attribute__((always_inline)) {
-        q4k_item_load(dst, p.wq, p.K, t0 + w, min(u, U - 1), g, r);
-    };
-    float dsc[8], dmm[8];
-    auto decode_b = [&](const Q4KItem &it, int pr, int buf) __attribute__((always_inline)) {
-        uint8_t *base = smem + buf * kGemmStageBytes + 32 * 1024 + lo16;
-        f16x8 lo, hi;
-        q4k_pair_frags(it, pr, dsc, dmm, lo, hi);
-        *(f16x8 *)(base + (w * 2 + 0) * 1024) = lo;
-        *(f16x8 *)(base + (w * 2 + 1) * 1024) = hi;
-    };
 
-    f32x4 acc[4][4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    auto mfma_stage = [&](int buf) __attribute__((always_inline)) {
-        const uint8_t *base = smem + buf * kGemmStageBytes + lo16;
-        // all 16 fragments of the stage first, so the reads of step 1 overlap step 0's MFMAs
-        f16x8 bf[2][4], af[2][4];
-#pragma unroll
-        for (int ss = 0; ss < 2; ++ss) {
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt)
-                bf[ss][nt] = *(const f16x8 *)(base + 32 * 1024 + ((4 * nh + nt) * 2 + ss) * 1024);
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-                af[ss][mt] = *(const f16x8 *)(base + ((4 * mq + mt) * 2 + ss) * 1024);
-        }
-#pragma unroll
-        for (int ss = 0; ss < 2; ++ss)
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-                for (int nt = 0; nt < 4; ++nt)
-                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[ss][mt], bf[ss][nt], acc[mt][nt], 0, 0, 0);
-    };
-
-    // prologue: stage 0 in buffer 0; activations of stage 1 and weights of block 1 in flight
-    Q4KItem cur, nxt;
-    u32x4 ra[4], rb[4];  // activation fragments of odd / even stages in flight
-    load_a(rb, 0);
+    // Register sets: own activation fragments of stages t .. t + 3 (index t % 4), own decoded
+    // weight fragments of stages t .. t + 2 (index t % 4), other fragments read from LDS for
+    // stages t, t + 1 (index t % 2).
+    Q4KItem cur[BS], nxt[BS];
+    u32x4 A[4][AS];
+    f16x8 B[4][BS];
+    f16x8 FA[2][MT - AS], FB[2][NT - BS];
     load_w(cur, 0);
-    load_a(ra, 1);
     load_w(nxt, 1);
-    store_a(rb, 0);
-    q4k_row_scales(cur.hv, g, dsc, dmm);
-    decode_b(cur, 0, 0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) load_a(A[t], t);
+    block_scales(cur);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int k = 0; k < BS; ++k) B[t][k] = q4k_sub_frag(cur[k], t, dsc[k][t], dmm[k][t]);
+        store_b(B[t], t);
+        store_a(A[t], t);
+    }
     lds_barrier();
+    read_other(FA[0], FB[0], 0);
 
-    // One step of the stage pipeline: MFMAs of stage st from buffer st & 1; stage st + 1 (its
-    // activations in `next`, issued a stage ago) decoded and stored into the other buffer;
-    // activations of stage st + 2 issued into `fresh`.
-    auto step = [&](int st, int pr, u32x4 *next, u32x4 *fresh) __attribute__((always_inline)) {
-        load_a(fresh, st + 2);
-        mfma_stage(pr & 1);
-        if (st + 1 < stages) {
-            if (pr == 3) {  // the next stage starts a block: its raw weights are in nxt
-                cur = nxt;
-                load_w(nxt, (st >> 2) + 2);
-                q4k_row_scales(cur.hv, g, dsc, dmm);
+    // Stage st (j = st % 8): read stage st + 1's other fragments, MFMAs of stage st, write
+    // stage st + 2 (decode its weight fragments, store its activation fragments), then load
+    // stage st + 4's activations into the registers stage st used. `tail` guards the stages
+    // near the end of K; the other stages are branch-free, and their instructions are
+    // interleaved so the decode, LDS traffic and loads issue between the MFMAs.
+    auto step = [&](int st, int j, bool tail) __attribute__((always_inline)) {
+        const int c = j & 3, f = j & 1;
+        const int j2 = (j + 2) & 7;
+        if (!tail || st + 1 < stages) read_other(FA[f ^ 1], FB[f ^ 1], st + 1);
+        if (!tail || st + 2 < stages) {
+            if (j2 == 0) {  // stage st + 2 starts a block: its raw weights are in nxt
+#pragma unroll
+                for (int k = 0; k < BS; ++k) cur[k] = nxt[k];
+                load_w(nxt, (st + 2) / 8 + 1);
+                block_scales(cur);
             }
-            decode_b(cur, (pr + 1) & 3, (pr & 1) ^ 1);
-            store_a(next, (pr & 1) ^ 1);
+#pragma unroll
+            for (int k = 0; k < BS; ++k) B[(c + 2) & 3][k] = q4k_sub_frag(cur[k], j2, dsc[k][j2], dmm[k][j2]);
+            store_b(B[(c + 2) & 3], st + 2);
+            store_a(A[(c + 2) & 3], st + 2);
+        }
+        mfma_stage(A[c], B[c], FA[f], FB[f]);
+        load_a(A[c], st + 4);
+        if (!tail && j2 != 0) {
+            constexpr int NM = MT * NT;                       // MFMAs of the stage
+            constexpr int NR = (MT - AS) + (NT - BS);         // LDS reads
+            constexpr int NW = AS + BS;                       // LDS writes
+            constexpr int NV = 3;                             // VALU per MFMA slot
+#pragma unroll
+            for (int i = 0; i < NM; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, NV, 0); // VALU
+                if (i < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                            // DS read
+                else if (i >= NM / 2 && i < NM / 2 + NW) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // DS write
+                else if (i >= NM - AS - 2 && i < NM - 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); // VMEM read
+            }
         }
         lds_barrier();
     };
-    for (int b = 0; b < U; ++b) {
-        step(4 * b + 0, 0, ra, rb);
-        step(4 * b + 1, 1, rb, ra);
-        step(4 * b + 2, 2, ra, rb);
-        step(4 * b + 3, 3, rb, ra);
+    for (int b = 0; b + 1 < U; ++b) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) step(8 * b + j, j, false);
     }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) step(8 * (U - 1) + j, j, true);
 
     // epilogue: lane (g, r) holds column r, rows 4g .. 4g + 3 of each 16 x 16 tile
     const bool f32_out = p.out_type == 0;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int i = 0; i < MT; ++i) {
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-            const int col = (t0 + 4 * nh + nt) * 16 + r;
+        for (int k = 0; k < NT; ++k) {
+            const int col = (t0 + n_of(k)) * 16 + r;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = (mt0 + 4 * mq + mt) * 16 + 4 * g + i;
+            for (int e = 0; e < 4; ++e) {
+                const int m = (mt0 + m_of(i)) * 16 + 4 * g + e;
                 if (m < p.M) {
                     const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
                     if (f32_out)
-                        ((float *)p.out)[o] = acc[mt][nt][i];
+                        ((float *)p.out)[o] = acc[i][k][e];
                     else
-                        ((uint16_t *)p.out)[o] = (uint16_t)f2bf(acc[mt][nt][i]);
+                        ((uint16_t *)p.out)[o] = (uint16_t)f2bf(acc[i][k][e]);
                 }
             }
         }
     }
 }
+
+extern "C" __global__ __launch_bounds__(512) void jv_gemm_q4k_256x128(GemmParams p) { gemm_q4k_body<4, 2>(p); }
 
 // ---------------------------------------------------------------------------------------------
 // Repack GGML blocks (device copy) into the device layouts above.

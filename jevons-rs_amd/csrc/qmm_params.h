@@ -41,13 +41,12 @@ struct PackXParams {
     int32_t mtiles;      // 16-row tiles packed (M rounded up to the product's row tile)
 };
 
-// Q4_K tiled product over packed activation fragments (jv_pack_x output).
+// Q4_K 256 x 128-tile product over packed activation fragments (jv_pack_x output).
 struct GemmParams {
     const uint16_t *xa;  // packed activations
     const uint8_t *wq;   // Q4_K tile layout
     void *out;           // [M][ldo] of `out_type`
     int32_t M, N, K, ldo, out_type;
-    int32_t mtiles;
 };
 
 // GGML blocks (device copy of the upload) -> device layout.
