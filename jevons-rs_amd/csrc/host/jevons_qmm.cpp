@@ -343,68 +343,36 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
     if (!x || !out) return fail(JV_ERR_INVALID, "null activation or output buffer");
     if (((uintptr_t)x & 15u) != 0) return fail(JV_ERR_INVALID, "activations must be 16-byte aligned");
 
-    // Small-row Q4_K kernels. Both sum a row's blocks in an order that does not depend on m,
-    // so every m takes the same kernel. The persistent kernel below is the default; JV_QMV2=WxP
-    // selects the per-tile kernel (W waves, P blocks in flight per wave), which is faster at
-    // m = 1 and slower from m = 4 on, where its per-tile activation staging costs occupancy.
-    const char *qmv2_env = getenv("JV_QMV2");
-    if (plan.bm == 0 && w->fmt == JV_FMT_Q4K && qmv2_env && m <= 16 &&
-        w->n * w->experts * w->k / 2 < (1ull << 32)) {
-        int waves = 8, pf = 2;
-        if (qmv2_env) sscanf(qmv2_env, "%dx%d", &waves, &pf);
-        if (!((waves == 4 && pf == 4) || (waves == 8 && pf == 2))) { waves = 8; pf = 2; }
+    // Small-row Q4_K kernel: one workgroup per one or two 16-row tiles (two from m = 3 on, which
+    // halves the activation staging per weight byte); both sum each output element the same way,
+    // so every output row is the same for any m.
+    if (plan.bm == 0 && w->fmt == JV_FMT_Q4K && w->n * w->experts * w->k / 2 < (1ull << 32)) {
+        const int tw = m <= 2 ? 1 : 2;
+        const int waves = 8;
         const int U = (int)(w->k / 256);
+        const int T = (int)(w->n * w->experts / 16);
         const int umax = (U + waves - 1) / waves;
-        const int refill = umax > pf ? 1 : 0;
-        const size_t lds = (size_t)waves * m * ((size_t)umax * 256 + 8) * 2 +
-                           (size_t)waves * m * umax * 8 * 4 + (size_t)waves * 64 * 16;
+        // per wave: FP16 activations [m][256 umax + 8] and sub-block sums [m][8 umax], then the
+        // wave's tile partials (tw KB); qmv_q4k_body computes the same size
+        const size_t stage = ((size_t)m * ((size_t)umax * 256 + 8) * 2 + (size_t)m * umax * 8 * 4 + 15) & ~(size_t)15;
+        const size_t lds = std::max(stage, (size_t)tw * 1024) * waves;
         if (lds <= ctx->info.lds_bytes) {
             QmmParams p{};
             p.x = x;
             p.out = out;
             p.wq = w->q;
             p.M = (int32_t)m;
-            p.N = (int32_t)w->n;
+            p.N = (int32_t)(w->n * w->experts);
             p.K = (int32_t)w->k;
             p.ldx = (int32_t)w->k;
-            p.ldo = (int32_t)w->n;
+            p.ldo = (int32_t)(w->n * w->experts);
             p.act = (int32_t)act;
             p.out_type = (int32_t)out_type;
             p.splits = 1;
             void *args[] = {&p};
-            char name[48];
-            snprintf(name, sizeof name, "jv_qmv2_q4k_w%d_p%d_m%d_r%d", waves, pf, m == 1 ? 1 : (m == 2 ? 2 : 4), refill);
-            return launch(ctx, name, dim3((unsigned)(w->n * w->experts / 16)), dim3((unsigned)(64 * waves)), lds, stream, args);
-        }
-    }
-    if (plan.bm == 0 && w->fmt == JV_FMT_Q4K && w->k <= 16384 && w->n * w->experts * w->k / 2 < (1ull << 32)) {
-        // Small-row Q4_K kernel: one 8-wave workgroup per compute unit stages the activations
-        // and their sub-block sums once and streams a contiguous range of 16-row tiles.
-        const int T = (int)(w->n / 16);
-        const int cus = std::max(1, ctx->info.compute_units);
-        int waves = 8, pf = 4, late = 0;
-        if (const char *e = getenv("JV_QMV_SHAPE")) sscanf(e, "%dx%dx%d", &waves, &pf, &late);
-        if (!((waves == 8 && (pf == 4 || pf == 8)) || (waves == 16 && pf == 4))) { waves = 8; pf = 4; }
-        late = late ? 1 : 0;
-        const size_t lds = m * (w->k + 8) * 2 + m * (w->k / 32) * 4 + (size_t)waves * 2 * 64 * 16;
-        if (lds <= ctx->info.lds_bytes) {
-            QmmParams p{};
-            p.x = x;
-            p.out = out;
-            p.wq = w->q;
-            p.M = (int32_t)m;
-            p.N = (int32_t)w->n;
-            p.K = (int32_t)w->k;
-            p.ldx = (int32_t)w->k;
-            p.ldo = (int32_t)w->n;
-            p.act = (int32_t)act;
-            p.out_type = (int32_t)out_type;
-            p.splits = 1;
-            const int grid = std::min(cus, T);
-            void *args[] = {&p};
-            char name[48];
-            snprintf(name, sizeof name, "jv_qmv_q4k_w%d_p%d_m%d_l%d", waves, pf, m == 1 ? 1 : (m == 2 ? 2 : 4), late);
-            return launch(ctx, name, dim3((unsigned)grid), dim3((unsigned)(64 * waves)), lds, stream, args);
+            char name[32];
+            snprintf(name, sizeof name, "jv_qmv_q4k_t%d_m%d", tw, m == 1 ? 1 : (m == 2 ? 2 : 4));
+            return launch(ctx, name, dim3((unsigned)((T + tw - 1) / tw)), dim3(64 * waves), lds, stream, args);
         }
     }
     if (plan.bm == 256) {

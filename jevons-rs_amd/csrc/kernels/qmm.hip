@@ -477,119 +477,19 @@ __device__ __forceinline__ void dequant_body(const DequantParams &p) {
 // ---------------------------------------------------------------------------------------------
 // Small-row Q4_K product (M <= 16) with exact integer weights.
 //
-// Per block and weight row, out += d * S - sum_j (1024 d + dmin m_j) X_j, where
-//   S   = sum_e x_e * (1024 + s_j q_e) over the block's 256 elements (one MFMA chain), the
-//         FP16 operand 1024 + s*q being exact (s <= 63, q <= 15) and built with one packed
-//         16-bit multiply-add on the bit pattern 0x6400 (= 1024.0);
-//   X_j = sum of the block's activations over sub-block j, prepared with the LDS staging;
-//   the correction is one FP32 MFMA 16x16x4 pair (k = sub-block).
-// This equals sum_e x_e * (d*s_j*q_e - dmin*m_j), the quant.rs:25-41 weights, up to FP32
-// rounding of the sums. Lane group g holds pair g of every block (sub-blocks 2g, 2g+1), so a
-// lane decodes two (scale, min) pairs per block. Activation fragments are stored in LDS with
-// each 8-element group in the order {0,2,1,3,4,6,5,7}, the order the nibble pairs come out of
-// a 32-bit word ((w & 0x000f000f) holds bytes 0 and 2).
-//
-// Each wave owns 16 weight rows over all of K; a workgroup of 4 waves owns 64 rows. Weight
-// loads run P blocks ahead of the MFMAs.
+// Per block and weight row, out += d * sum_j s'_j S_j - sum_j (1024 d s'_j + dmin m_j) X_j, where
+//   S_j = sum_e x_e * (1024 + q_e) over sub-block j (32 elements, one MFMA 16x16x32 f16), the
+//         FP16 operand 1024 + q being exact and built with one and-or on the bit pattern
+//         0x6400 (= 1024.0): low nibbles give 1024 + q, high nibbles 1024 + 16 q;
+//   s'_j = s_j for even j and s_j / 16 for odd j (high nibbles carry 16 q);
+//   X_j = sum of the activations over sub-block j, prepared with the LDS staging;
+//   the bias terms are one FP32 MFMA 16x16x4 pair (k = sub-block).
+// This equals sum_e x_e * (d*s_j*q_e - dmin*m_j), the quant.rs:25-41 weights times x, up to FP32
+// rounding of the sums: the products x * (1024 + q) are exact, and the 1024 X_j term cancels
+// against the sums' 1024 x_e parts to FP32 rounding. The device layout stores each 4-byte group of
+// quant bytes in the order {0, 2, 1, 3}, so (w & 0x000f000f) holds two consecutive elements and
+// the activation fragments are read in natural order.
 // ---------------------------------------------------------------------------------------------
-typedef short s16x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t pk_mad_u16(uint32_t a, uint32_t b, uint32_t c) {
-    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-    u16x2 r = __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b) + __builtin_bit_cast(u16x2, c);
-    return __builtin_bit_cast(uint32_t, r);
-}
-
-// Loads are issued unconditionally (clamped to the last chunk) so the compiler can count
-// outstanding loads exactly and wait only for the ones it needs.
-template <int ACT, int NTHR, bool LATE, class After>
-__device__ __forceinline__ void stage_q4k_rows_act(const QmmParams &p, _Float16 *xs, float *Xs,
-                                                   After after) {
-    constexpr int XB = ACT == 2 ? 4 : 8;  // 16-byte loads per thread held at once
-    constexpr int EPL = ACT == 2 ? 4 : 8;  // elements per load
-    const int per_row = p.K >> 3;
-    const int total = p.M * per_row;  // 8-element chunks; multiple of 4 (K % 64 == 0)
-    const int stride = p.K + kLdsPad;
-    constexpr int nthr = NTHR;
-    bool issued = false;
-    for (int i0 = 0; i0 < total; i0 += XB * nthr) {
-        uint4 raw[XB][8 / EPL];
-        const int nq = min(XB, (total - i0 + nthr - 1) / nthr);  // batches with real chunks
-#pragma unroll
-        for (int q = 0; q < XB; ++q) {
-            if (q >= nq) break;  // uniform: later batches hold no chunk for any thread
-            const int i = min(i0 + q * nthr + (int)threadIdx.x, total - 1);
-            const int r = i / per_row;
-            const int c8 = i - r * per_row;
-            const size_t src = (size_t)r * (size_t)p.ldx + (size_t)(8 * c8);
-#pragma unroll
-            for (int hh = 0; hh < 8 / EPL; ++hh) {
-                if (ACT == 2)
-                    raw[q][hh] = *(const uint4 *)((const float *)p.x + src + 4 * hh);
-                else
-                    raw[q][hh] = *(const uint4 *)((const uint16_t *)p.x + src);
-            }
-        }
-        if (!issued && !LATE) {
-            after();
-            issued = true;
-        }
-#pragma unroll
-        for (int q = 0; q < XB; ++q) {
-            if (q >= nq) break;
-            const int i = i0 + q * nthr + (int)threadIdx.x;
-            float part = 0.f;
-            int r = 0, c8 = 0;
-            if (i < total) {
-                r = i / per_row;
-                c8 = i - r * per_row;
-                float v[8];
-                if (ACT == 2) {
-                    const uint32_t w[8] = {raw[q][0].x, raw[q][0].y, raw[q][0].z, raw[q][0].w,
-                                           raw[q][8 / EPL - 1].x, raw[q][8 / EPL - 1].y,
-                                           raw[q][8 / EPL - 1].z, raw[q][8 / EPL - 1].w};
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = __builtin_bit_cast(float, w[e]);
-                } else {
-                    const uint32_t w[4] = {raw[q][0].x, raw[q][0].y, raw[q][0].z, raw[q][0].w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        v[2 * e] = ACT == 0 ? h2f(w[e]) : bf2f(w[e]);
-                        v[2 * e + 1] = ACT == 0 ? h2f(w[e] >> 16) : bf2f(w[e] >> 16);
-                    }
-                }
-                f16x8 h;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) h[e] = (_Float16)v[e];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) part += (float)h[e];
-                *(f16x8 *)(xs + r * stride + 8 * c8) = h;
-            }
-            // four consecutive 8-element chunks (lanes 4j..4j+3) form one 32-element sub-block
-            part += __shfl_xor(part, 1);
-            part += __shfl_xor(part, 2);
-            if (i < total && (c8 & 3) == 0) Xs[r * (p.K >> 5) + (c8 >> 2)] = part;
-        }
-    }
-    if (!issued) after();
-}
-
-// Stages activation rows [0, M) x [0, K) as FP16 plus FP32 sums over each 32-element
-// sub-block (xs row stride K + 8 elements, Xs row stride K / 32). The activation loads are issued
-// first and `after()` (the weight loads) next, so the activations do not queue behind the
-// weight stream.
-// LATE: `after()` runs once the activations are converted instead of right after their loads.
-template <int NTHR, bool LATE, class After>
-__device__ __forceinline__ void stage_q4k_rows_first(const QmmParams &p, _Float16 *xs, float *Xs,
-                                                     After after) {
-    if (p.act == 0)
-        stage_q4k_rows_act<0, NTHR, LATE>(p, xs, Xs, after);
-    else if (p.act == 1)
-        stage_q4k_rows_act<1, NTHR, LATE>(p, xs, Xs, after);
-    else
-        stage_q4k_rows_act<2, NTHR, LATE>(p, xs, Xs, after);
-}
-
 // Q4_K (scale, min) of sub-blocks 2g and 2g+1, branch-free (quant.rs:14-23): lane groups
 // 0-1 hold sub-blocks 0-3 (low form), groups 2-3 sub-blocks 4-7 (high form).
 __device__ __forceinline__ void q4k_pair_scales(const uint4 &hd, int g, uint32_t sc[2], uint32_t mn[2]) {
@@ -633,173 +533,6 @@ __device__ __forceinline__ uint4 q4k_head_gather(uint32_t hv) {
     const auto e = __builtin_amdgcn_permlane32_swap(x[0], x[0], false, false);  // d0, d2 everywhere
     const auto o = __builtin_amdgcn_permlane32_swap(x[1], x[1], false, false);  // d1, d3 everywhere
     return uint4{(uint32_t)e[0], (uint32_t)o[0], (uint32_t)e[1], (uint32_t)o[1]};
-}
-
-// One Q4_K block of 16 weight rows against the staged activations: acc += products.
-// Sub-block j is one MFMA on exact operands 1024 + q (even j, low nibbles, bits 0-3) or
-// 1024 + 16 q (odd j, high nibbles, bits 4-7), each built with a single and-or on the bit
-// pattern 0x6400 (= 1024.0); S_j is scaled by A'_j = d s_j (/16 for odd j) and the bias and
-// min terms sum_j (1024 A'_j + dmin m_j) X_j come from one FP32 MFMA 16x16x4 pair, where
-// X_j is the sub-block's activation sum. This equals the quant.rs:25-41 weights times x, up
-// to FP32 rounding of the sums. Lane group g decodes sub-blocks 2g, 2g+1 and reads the other
-// scales from their lane groups with ds_bpermute. Only output rows 4g + i, i < MV, are kept.
-template <int MV>
-__device__ __forceinline__ void q4k_block_v6(const Q4KItem &cur, const _Float16 *xrow,
-                                             const float *Xrow, int u, int g, int r16, f32x4 &acc) {
-    const uint4 hd = q4k_head_gather(cur.hv);
-    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-    uint32_t sc[2], mn[2];
-    q4k_pair_scales(hd, g, sc, mn);
-    const float a0 = d * (float)sc[0];              // A'_{2g}
-    const float a1 = d * (float)sc[1] * 0.0625f;    // A'_{2g+1}: high nibbles carry 16 q
-    const float c0 = -__builtin_fmaf(1024.f, a0, dmin * (float)mn[0]);
-    const float c1 = -__builtin_fmaf(1024.f, a1, dmin * (float)mn[1]);
-    float aj[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int src = ((j >> 1) * 16 + r16) * 4;
-        aj[j] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
-                                              src, __builtin_bit_cast(int, (j & 1) ? a1 : a0)));
-    }
-    const uint32_t w[8] = {cur.q0.x, cur.q0.y, cur.q0.z, cur.q0.w, cur.q1.x, cur.q1.y, cur.q1.z, cur.q1.w};
-    const int kb = u * 256 + 8 * g;
-    // The magic held in a register lets each operand word be one v_and_or_b32 (a VOP3 op
-    // cannot encode two 32-bit literals on this architecture).
-    uint32_t magic = 0x64006400u;
-    asm("" : "+v"(magic));
-    // All eight sub-block products are independent: issue every MFMA into its own result
-    // registers first and scale afterwards, so the matrix unit runs them back to back.
-    f32x4 S[8];
-#pragma unroll
-    for (int pr = 0; pr < 4; ++pr) {
-        const uint32_t wa = w[2 * pr], wb = w[2 * pr + 1];
-        const uint32_t wa8 = wa >> 8, wb8 = wb >> 8;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int j = 2 * pr + h;
-            const uint32_t mask = h ? 0x00f000f0u : 0x000f000fu;
-            uint4 bq;
-            bq.x = (wa & mask) | magic;
-            bq.y = (wa8 & mask) | magic;
-            bq.z = (wb & mask) | magic;
-            bq.w = (wb8 & mask) | magic;
-            const f16x8 a = *(const f16x8 *)(xrow + kb + 32 * j);
-            S[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                a, __builtin_bit_cast(f16x8, bq), f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int i = 0; i < MV; ++i) acc[i] = __builtin_fmaf(aj[j], S[j][i], acc[i]);
-    // bias and min terms: k index = lane group g, sub-block 2g + t
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[u * 8 + 2 * g], c0, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[u * 8 + 2 * g + 1], c1, acc, 0, 0, 0);
-}
-
-// Persistent small-row Q4_K kernel. Workgroup c (one per compute unit, W waves) owns tiles
-// [c*T/G, (c+1)*T/G) of 16 weight rows. Their (tile, block) list, tile-major, is cut into W
-// contiguous slices, one per wave. The activations are staged first; then each wave streams
-// its slice with its weight loads P blocks ahead of the MFMAs. Loads are unconditional (past
-// the slice end a slot reloads the slice's last block) so waits are exact. A wave writes the
-// tiles it covers completely; a tile cut between waves leaves partials in LDS that the wave
-// where the tile starts sums in wave order, so results are deterministic and independent of M.
-template <int W, int P, int MV, bool LATE>
-__device__ __forceinline__ void qmv_q4k_body(const QmmParams &p) {
-    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int g = lane >> 4;
-    const int r16 = lane & 15;
-    const int U = p.K >> 8;
-    const int T = p.N >> 4;
-    const int t_begin = (int)((int64_t)blockIdx.x * T / gridDim.x);
-    const int t_end = (int)((int64_t)(blockIdx.x + 1) * T / gridDim.x);
-    const int n_items = (t_end - t_begin) * U;
-    const int a = wave * n_items / W, b = (wave + 1) * n_items / W;
-    const int stride = p.K + kLdsPad;
-    _Float16 *xs = lds;
-    float *Xs = (float *)(lds + p.M * stride);
-    f32x4 *part = (f32x4 *)(Xs + p.M * (p.K >> 5));  // [W][2][64]
-
-    // item idx of the slice (clamped to its last item; an empty slice loads item 0)
-    auto load_item = [&](Q4KItem &dst, int idx) {
-        idx = b > a ? min(idx, b - 1) : 0;
-        q4k_item_load(dst, p.wq, p.K, t_begin + idx / U, idx % U, g, r16);
-    };
-    Q4KItem buf[P];
-    stage_q4k_rows_first<64 * W, LATE>(p, xs, Xs, [&] {
-#pragma unroll
-        for (int j = 0; j < P; ++j) load_item(buf[j], a + j);
-    });
-    lds_barrier();
-
-    const int arow = min(r16, p.M - 1);  // rows >= M feed output rows that are never stored
-    const _Float16 *xrow = xs + arow * stride;
-    const float *Xrow = Xs + arow * (p.K >> 5);
-
-    auto store = [&](int tile, const f32x4 &v) {
-        const int col = tile * 16 + r16;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = 4 * g + i;
-            if (m < p.M) {
-                const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
-                if (p.out_type == 0)
-                    ((float *)p.out)[o] = v[i];
-                else
-                    ((uint16_t *)p.out)[o] = (uint16_t)f2bf(v[i]);
-            }
-        }
-    };
-
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    int nparts = 0;
-    int u = a % U, trel = a / U;  // block and tile (relative) of the current item
-    for (int i0 = a; i0 < b; i0 += P) {
-#pragma unroll
-        for (int j = 0; j < P; ++j) {
-            const int idx = i0 + j;
-            if (idx < b) {
-                q4k_block_v6<MV>(buf[j], xrow, Xrow, u, g, r16, acc);
-                if (u == U - 1 || idx == b - 1) {  // end of this wave's share of a tile
-                    if (idx - u >= a && u == U - 1) {
-                        store(t_begin + trel, acc);
-                    } else {
-                        part[(wave * 2 + nparts) * 64 + lane] = acc;
-                        ++nparts;
-                    }
-                    acc = f32x4{0.f, 0.f, 0.f, 0.f};
-                }
-                if (++u == U) {
-                    u = 0;
-                    ++trel;
-                }
-            }
-            load_item(buf[j], idx + P);  // refill the freed slot P items ahead
-        }
-    }
-    lds_barrier();
-    // A tile cut between waves starts in one slice (the wave's tail partial) and continues as
-    // the first partial of the following waves. The wave where it starts combines it.
-    if (a < b) {
-        const int last_tile = (b - 1) / U;
-        if ((b - 1) % U != U - 1 && last_tile * U >= a) {
-            const int tail = (a % U) != 0 ? 1 : 0;  // a head partial comes first
-            f32x4 sum = part[(wave * 2 + tail) * 64 + lane];
-            const int tile_end = (last_tile + 1) * U;
-            for (int w = wave + 1; w < W; ++w) {
-                const int wa = w * n_items / W, wb = (w + 1) * n_items / W;
-                if (wa >= tile_end) break;
-                if (wa < wb) {
-                    const f32x4 v = part[(w * 2) * 64 + lane];  // w's first partial
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) sum[i] += v[i];
-                }
-            }
-            store(t_begin + last_tile, sum);
-        }
-    }
 }
 
 // Stages columns [c0, c0 + ncols) of activation rows [0, M) for one wave: FP16 into
@@ -867,8 +600,10 @@ __device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int 
                 f16x8 h;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) h[e] = (_Float16)v[e];
+                // FP32 sum of the FP16 values, two per dot-product step
 #pragma unroll
-                for (int e = 0; e < 8; ++e) part += (float)h[e];
+                for (int e = 0; e < 4; ++e)
+                    part = __builtin_amdgcn_fdot2(f16x2{h[2 * e], h[2 * e + 1]}, f16x2{1.0f16, 1.0f16}, part, false);
                 *(f16x8 *)(xs + r * stride + 8 * c8) = h;
             }
             // lanes 4q..4q+3 hold the four 8-element chunks of one 32-element sub-block
@@ -880,36 +615,115 @@ __device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int 
     if (!issued) after();
 }
 
-// Small-row Q4_K kernel, one workgroup per 16-row tile. Wave w of W owns blocks
-// [w U / W, (w+1) U / W) of the tile (U = K / 256): it issues its activation loads, then its
-// first P weight blocks, stages its own activation columns in a private LDS region (no
-// workgroup barrier), and runs the blocks as they arrive, refilling P blocks ahead when
-// REFILL. The W partial sums are added in wave order by wave 0, so results are deterministic
-// and each output row is independent of M. Many short workgroups, each reading one contiguous
-// 16-row tile, keep the HBM queues fuller than long-lived per-CU workgroups do.
-template <int W, int P, int MV, int XB, bool REFILL>
-__device__ __forceinline__ void qmv2_q4k_body(const QmmParams &p) {
+// One block against activations staged in LDS, with the scale arithmetic regrouped to cut
+// vector ALU work (the kernel is bound by it once the loads are in flight):
+//   out += d * (sum_even s_j S_j + (sum_odd s_j S_j) / 16) - sum_j (1024 d s'_j + dmin m_j) X_j,
+// the eight 6-bit scales unpacked with byte masks, and the bias terms of sub-blocks g and
+// 4 + g (lane group g; k index g of the two FP32 MFMAs 16x16x4) extracted with lane-variable
+// shifts sh = 8 g. kfac = -1024 for even g, -64 for odd g (sub-blocks g and 4 + g hold high
+// nibbles, 16 q, when g is odd). The result equals quant.rs:25-41's weights times x up to FP32
+// rounding of the sums; each output row's arithmetic is the same for every M.
+template <int MV>
+__device__ __forceinline__ void q4k_block_fast(const Q4KItem &cur, const _Float16 *xrow,
+                                               const float *Xrow, int ul, int g, uint32_t sh,
+                                               float kfac, f32x4 &acc) {
+    const uint4 hd = q4k_head_gather(cur.hv);
+    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+    // scale bytes: y = q[0..3], z = q[4..7], w = q[8..11] (quant.rs:14-23)
+    const uint32_t s_lo = hd.y & 0x3f3f3f3fu;                                   // s_0..s_3
+    const uint32_t s_hi = ((hd.y >> 2) & 0x30303030u) | (hd.w & 0x0f0f0f0fu);    // s_4..s_7
+    const uint32_t m_hi = ((hd.z >> 2) & 0x30303030u) | ((hd.w >> 4) & 0x0f0f0f0fu);  // m_4..m_7
+    const float sg = (float)((s_lo >> sh) & 0xffu), s4g = (float)((s_hi >> sh) & 0xffu);
+    const float mg = (float)((hd.z >> sh) & 63u), m4g = (float)((m_hi >> sh) & 0xffu);
+    const float kd = kfac * d;
+    const float cA = __builtin_fmaf(kd, sg, -(dmin * mg));
+    const float cB = __builtin_fmaf(kd, s4g, -(dmin * m4g));
+    float sj[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        sj[k] = (float)((s_lo >> (8 * k)) & 0xffu);
+        sj[4 + k] = (float)((s_hi >> (8 * k)) & 0xffu);
+    }
+    uint32_t magic = 0x64006400u;
+    asm("" : "+v"(magic));
+    const int kb = ul * 256 + 8 * g;
+    const uint32_t w[8] = {cur.q0.x, cur.q0.y, cur.q0.z, cur.q0.w, cur.q1.x, cur.q1.y, cur.q1.z, cur.q1.w};
+    float ve[MV], vo[MV];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+        f32x4 S[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int j = 4 * hf + q;
+            const uint32_t wa = w[j & ~1], wb = w[(j & ~1) + 1];
+            const uint32_t mask = (j & 1) ? 0x00f000f0u : 0x000f000fu;
+            uint4 bq;
+            bq.x = (wa & mask) | magic;
+            bq.y = ((wa >> 8) & mask) | magic;
+            bq.z = (wb & mask) | magic;
+            bq.w = ((wb >> 8) & mask) | magic;
+            S[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xrow + kb + 32 * j),
+                                                          __builtin_bit_cast(f16x8, bq),
+                                                          f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < MV; ++i) {
+            if (hf == 0) {
+                ve[i] = sj[0] * S[0][i];
+                vo[i] = sj[1] * S[1][i];
+            } else {
+                ve[i] = __builtin_fmaf(sj[4], S[0][i], ve[i]);
+                vo[i] = __builtin_fmaf(sj[5], S[1][i], vo[i]);
+            }
+            ve[i] = __builtin_fmaf(sj[4 * hf + 2], S[2][i], ve[i]);
+            vo[i] = __builtin_fmaf(sj[4 * hf + 3], S[3][i], vo[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MV; ++i) acc[i] = __builtin_fmaf(d, __builtin_fmaf(vo[i], 0.0625f, ve[i]), acc[i]);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[ul * 8 + g], cA, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[ul * 8 + 4 + g], cB, acc, 0, 0, 0);
+}
+
+// Small-row Q4_K kernel, one workgroup per TW consecutive 16-row tiles. Wave w of W owns blocks
+// [w U / W, (w+1) U / W) (U = K / 256) of every tile of the workgroup: it issues its activation
+// loads, then its first P (tile, block) items, stages its own activation columns in a private LDS
+// region (no workgroup barrier), and runs the items as they arrive, tile-major, refilling P
+// items ahead when they do not all fit. A wave's partial sum of each tile goes to its own LDS
+// region; after one barrier, wave t adds tile t's W partials in wave order. Each output element
+// is the same sum for every M and TW. Many short workgroups keep every compute unit fed as the
+// memory system serves them unevenly.
+template <int W, int TW, int P, int MV, int XB>
+__device__ __forceinline__ void qmv_q4k_body(const QmmParams &p) {
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4;
     const int r16 = lane & 15;
     const int U = p.K >> 8;
-    const int tile = blockIdx.x;
+    const int T = p.N >> 4;
+    const int tile0 = blockIdx.x * TW;
+    const int ntw = min(TW, T - tile0);  // tiles of this workgroup (>= 1)
     const int u0 = wave * U / W;
     const int nu = (wave + 1) * U / W - u0;
     const int umax = (U + W - 1) / W;
     const int stride = umax * 256 + kLdsPad;
     const int xstride = umax * 8;
-    _Float16 *xs = lds + wave * p.M * stride;
-    float *Xall = (float *)(lds + W * p.M * stride);
-    float *Xs = Xall + wave * p.M * xstride;
-    f32x4 *part = (f32x4 *)(Xall + W * p.M * xstride);  // [W][64]
+    // per wave: FP16 activations [M][stride], then sums [M][xstride]; reused for the partials
+    const int region = max((p.M * stride * 2 + p.M * xstride * 4 + 15) & ~15, TW * 1024);  // bytes
+    uint8_t *mine = (uint8_t *)lds + (size_t)wave * region;
+    _Float16 *xs = (_Float16 *)mine;
+    float *Xs = (float *)(mine + p.M * stride * 2);
+    const int nitems = nu * ntw;
 
     auto load_item = [&](Q4KItem &dst, int idx) {
-        q4k_item_load(dst, p.wq, p.K, tile, u0 + min(idx, nu - 1), g, r16);
+        idx = min(idx, nitems - 1);
+        const int tw = idx / nu;
+        q4k_item_load(dst, p.wq, p.K, tile0 + tw, u0 + (idx - tw * nu), g, r16);
     };
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[TW];
+#pragma unroll
+    for (int t = 0; t < TW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (nu > 0) {
         Q4KItem buf[P];
         auto issue = [&] {
@@ -929,39 +743,50 @@ __device__ __forceinline__ void qmv2_q4k_body(const QmmParams &p) {
         const int arow = min(r16, p.M - 1);  // rows >= M feed output rows that are never stored
         const _Float16 *xrow = xs + arow * stride;
         const float *Xrow = Xs + arow * xstride;
-        if (REFILL) {
-            for (int i0 = 0; i0 < nu; i0 += P) {
+        const uint32_t sh = 8u * (uint32_t)g;
+        const float kfac = (g & 1) ? -64.f : -1024.f;
+        for (int i0 = 0; i0 < nitems; i0 += P) {
 #pragma unroll
-                for (int j = 0; j < P; ++j) {
-                    const int idx = i0 + j;
-                    if (idx < nu) q4k_block_v6<MV>(buf[j], xrow, Xrow, idx, g, r16, acc);
-                    load_item(buf[j], idx + P);
+            for (int j = 0; j < P; ++j) {
+                const int idx = i0 + j;
+                if (idx < nitems) {
+                    const int tw = idx / nu;
+                    f32x4 a = acc[0];
+#pragma unroll
+                    for (int t = 1; t < TW; ++t)
+                        if (t == tw) a = acc[t];
+                    q4k_block_fast<MV>(buf[j], xrow, Xrow, idx - tw * nu, g, sh, kfac, a);
+#pragma unroll
+                    for (int t = 0; t < TW; ++t)
+                        if (t == tw) acc[t] = a;
                 }
+                if (i0 + P < nitems) load_item(buf[j], idx + P);
             }
-        } else {  // nu <= P: every block is already in flight
-#pragma unroll
-            for (int j = 0; j < P; ++j)
-                if (j < nu) q4k_block_v6<MV>(buf[j], xrow, Xrow, j, g, r16, acc);
         }
     }
-    if (wave > 0) part[wave * 64 + lane] = acc;
-    lds_barrier();
-    if (wave == 0) {
-        for (int w = 1; w < W; ++w) {
-            const f32x4 v = part[w * 64 + lane];
+    // this wave's staging region is no longer read: it takes the partials
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    f32x4 *part = (f32x4 *)mine;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] += v[i];
+    for (int t = 0; t < TW; ++t) part[t * 64 + lane] = acc[t];
+    lds_barrier();
+    for (int t = wave; t < ntw; t += W) {
+        f32x4 sum = ((const f32x4 *)lds)[t * 64 + lane];
+        for (int w = 1; w < W; ++w) {
+            const f32x4 v = ((const f32x4 *)((const uint8_t *)lds + (size_t)w * region))[t * 64 + lane];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum[i] += v[i];
         }
-        const int col = tile * 16 + r16;
+        const int col = (tile0 + t) * 16 + r16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int m = 4 * g + i;
             if (m < p.M) {
                 const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
                 if (p.out_type == 0)
-                    ((float *)p.out)[o] = acc[i];
+                    ((float *)p.out)[o] = sum[i];
                 else
-                    ((uint16_t *)p.out)[o] = (uint16_t)f2bf(acc[i]);
+                    ((uint16_t *)p.out)[o] = (uint16_t)f2bf(sum[i]);
             }
         }
     }
@@ -969,29 +794,19 @@ __device__ __forceinline__ void qmv2_q4k_body(const QmmParams &p) {
 
 }  // namespace
 
-#define JV_QMV2(W, P, MV, XB, R)                                                              \
-    extern "C" __global__ __launch_bounds__(64 * W) void jv_qmv2_q4k_w##W##_p##P##_m##MV##_r##R( \
-        QmmParams p) {                                                                        \
-        qmv2_q4k_body<W, P, MV, XB, R == 1>(p);                                               \
+// One-tile workgroups run four per compute unit (8 waves per SIMD, at most 64 VGPRs); the
+// library takes them for M <= 2 and two-tile workgroups (half the activation staging per weight
+// byte) for larger M. MV = output rows kept per lane group (M = 1, 2, or up to 16).
+#define JV_QMV(TW, MV, XB)                                                                   \
+    extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(TW == 1 ? 8 : 4))) \
+    void jv_qmv_q4k_t##TW##_m##MV(QmmParams p) {                                             \
+        qmv_q4k_body<8, TW, 2 * TW, MV, XB>(p);                                             \
     }
-#define JV_QMV2_M(W, P, R) JV_QMV2(W, P, 1, 2, R) JV_QMV2(W, P, 2, 4, R) JV_QMV2(W, P, 4, 8, R)
-JV_QMV2_M(4, 4, 0)
-JV_QMV2_M(4, 4, 1)
-JV_QMV2_M(8, 2, 0)
-JV_QMV2_M(8, 2, 1)
-
-#define JV_QMV(W, P, MV, L)                                                                \
-    extern "C" __global__ __launch_bounds__(64 * W) void jv_qmv_q4k_w##W##_p##P##_m##MV##_l##L( \
-        QmmParams p) {                                                                        \
-        qmv_q4k_body<W, P, MV, L == 1>(p);                                                    \
-    }
-#define JV_QMV_M(W, P, L) JV_QMV(W, P, 1, L) JV_QMV(W, P, 2, L) JV_QMV(W, P, 4, L)
-JV_QMV_M(8, 4, 0)
-JV_QMV_M(8, 8, 0)
-JV_QMV_M(8, 4, 1)
-JV_QMV_M(8, 8, 1)
-JV_QMV_M(16, 4, 0)
-JV_QMV_M(16, 4, 1)
+JV_QMV(1, 1, 2)
+JV_QMV(1, 2, 4)
+JV_QMV(2, 1, 4)
+JV_QMV(2, 2, 4)
+JV_QMV(2, 4, 8)
 
 // ---------------------------------------------------------------------------------------------
 // Entry points (looked up by name with hipModuleGetFunction).
