@@ -203,7 +203,7 @@ Layout layout_for(jv_fmt fmt, size_t blocks) {
     switch (fmt) {
     case JV_FMT_Q4K: l.q = blocks * 144; break;
     case JV_FMT_Q6K: l.q = blocks * 208; l.d = blocks * 2; break;
-    case JV_FMT_Q8_0: l.q = blocks * 32; l.d = blocks * 2; break;
+    case JV_FMT_Q8_0: l.q = blocks * 34; break;
     case JV_FMT_Q5_0: l.q = blocks * 16; l.h = blocks * 4; l.d = blocks * 2; break;
     default: break;
     }
@@ -283,17 +283,20 @@ jv_status build_from_device(jv_ctx *ctx, uint32_t type, jv_fmt fmt, size_t n, si
         rp.wh = base + oh;
         rp.wd = base + od;
         const char *name = nullptr;
+        int32_t kchunks = 0;
+        void *args[2] = {&rp, nullptr};
         if (fmt == JV_FMT_Q6K) {
             rp.chunks = (int64_t)blocks;
             name = "jv_repack_q6k";
         } else if (fmt == JV_FMT_Q8_0) {
             rp.chunks = (int64_t)(blocks / 2);
             name = "jv_repack_q8_0";
+            kchunks = (int32_t)(k / 64);
+            args[1] = &kchunks;
         } else {
             rp.chunks = (int64_t)(blocks / 2);
             name = "jv_repack_q5_0";
         }
-        void *args[] = {&rp};
         dim3 grid((unsigned)((rp.chunks + 255) / 256));
         st = launch(ctx, name, grid, dim3(256), 0, nullptr, args);
         if (st == JV_OK) {
@@ -343,18 +346,22 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
     if (!x || !out) return fail(JV_ERR_INVALID, "null activation or output buffer");
     if (((uintptr_t)x & 15u) != 0) return fail(JV_ERR_INVALID, "activations must be 16-byte aligned");
 
-    // Small-row Q4_K kernel: one workgroup per one or two 16-row tiles (two from m = 3 on, which
-    // halves the activation staging per weight byte); both sum each output element the same way,
-    // so every output row is the same for any m.
-    if (plan.bm == 0 && w->fmt == JV_FMT_Q4K && w->n * w->experts * w->k / 2 < (1ull << 32)) {
+    // Small-row Q4_K and Q8_0 kernels: one workgroup per one or two 16-row tiles (two from m = 3
+    // on, which halves the activation staging per weight byte); both sum each output element the
+    // same way, so every output row is the same for any m.
+    if (plan.bm == 0 && (w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q8_0) &&
+        w->n * w->experts * w->k < (1ull << 32)) {
+        const bool q4k = w->fmt == JV_FMT_Q4K;
         const int tw = m <= 2 ? 1 : 2;
-        const int waves = 8;
-        const int U = (int)(w->k / 256);
+        const int waves = q4k ? 8 : 16;
+        const int ku = q4k ? 256 : 64;  // K per item; activation sums per 32 columns
+        const int U = (int)(w->k / ku);
         const int T = (int)(w->n * w->experts / 16);
         const int umax = (U + waves - 1) / waves;
-        // per wave: FP16 activations [m][256 umax + 8] and sub-block sums [m][8 umax], then the
-        // wave's tile partials (tw KB); qmv_q4k_body computes the same size
-        const size_t stage = ((size_t)m * ((size_t)umax * 256 + 8) * 2 + (size_t)m * umax * 8 * 4 + 15) & ~(size_t)15;
+        // per wave: FP16 activations [m][ku umax + 8] and sums [m][ku umax / 32], then the wave's
+        // tile partials (tw KB); qmv_body computes the same size
+        const size_t stage = ((size_t)m * ((size_t)umax * ku + 8) * 2 + (size_t)m * umax * (ku / 32) * 4 + 15) &
+                             ~(size_t)15;
         const size_t lds = std::max(stage, (size_t)tw * 1024) * waves;
         if (lds <= ctx->info.lds_bytes) {
             QmmParams p{};
@@ -371,7 +378,8 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
             p.splits = 1;
             void *args[] = {&p};
             char name[32];
-            snprintf(name, sizeof name, "jv_qmv_q4k_t%d_m%d", tw, m == 1 ? 1 : (m == 2 ? 2 : 4));
+            snprintf(name, sizeof name, "jv_qmv_%s_t%d_m%d", q4k ? "q4k" : "q8_0", tw,
+                     m == 1 ? 1 : (m == 2 ? 2 : 4));
             return launch(ctx, name, dim3((unsigned)((T + tw - 1) / tw)), dim3(64 * waves), lds, stream, args);
         }
     }

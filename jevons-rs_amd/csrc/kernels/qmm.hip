@@ -208,9 +208,11 @@ struct FQ6K {
     }
 };
 
-// Q8_0, device layout: per 64 k (two blocks) 64 quant bytes; bytes 16g..16g+15 hold
-// block0[8g, +8) then block1[8g, +8). FP16 scales per block in the d region.
-// Step s (0, 1) is block s; elements 32s + 8g + e (quant.rs:75-80).
+// Q8_0, device layout: 16-row tiles, per 64 k (two blocks) 1088 bytes: [0, 1024) lane 16g + r
+// holds row r's block-0 elements 8g .. 8g+7 then its block-1 elements 8g .. 8g+7, as q + 128
+// (the quant byte xor 0x80), in the order {0, 2, 1, 3} within each 4-byte group; [1024, 1088)
+// the rows' two FP16 scales (4 bytes per row). Step s (0, 1) is block s; elements 32s + 8g + e
+// (quant.rs:75-80).
 struct FQ8_0 {
     static constexpr int KU = 64;
     struct Raw {
@@ -220,11 +222,12 @@ struct FQ8_0 {
     struct Prep {
         float d[2];
     };
-    __device__ static void load(Raw &r, const uint8_t *wq, const uint8_t *, const uint8_t *wd,
+    __device__ static void load(Raw &r, const uint8_t *wq, const uint8_t *, const uint8_t *,
                                 int K, int row, int u, int g) {
-        const size_t ch = (size_t)row * (size_t)(K / 64) + (size_t)u;
-        r.q = ld16(wq + ch * 64u + 16 * g);
-        r.d2 = *(const uint32_t *)(wd + ch * 4u);
+        const uint8_t *tb = wq + ((size_t)(row >> 4) * (size_t)(K / 64) + (size_t)u) * 1088u;
+        const int rr = row & 15;
+        r.q = ld16(tb + (16 * g + rr) * 16);
+        r.d2 = *(const uint32_t *)(tb + 1024 + 4 * rr);
     }
     __device__ static void prep(const Raw &r, Prep &p, int) {
         p.d[0] = h2f(r.d2);
@@ -235,7 +238,8 @@ struct FQ8_0 {
         const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int32_t q = (int32_t)(int8_t)((w[2 * s + (e >> 2)] >> (8 * (e & 3))) & 0xffu);
+            const int pos = ((e & 1) << 1) | ((e >> 1) & 1);  // stored byte of element e & 3
+            const int32_t q = (int32_t)((w[2 * s + (e >> 2)] >> (8 * pos)) & 0xffu) - 128;
             v[e] = p.d[s] * (float)q;
         }
     }
@@ -536,10 +540,10 @@ __device__ __forceinline__ uint4 q4k_head_gather(uint32_t hv) {
 }
 
 // Stages columns [c0, c0 + ncols) of activation rows [0, M) for one wave: FP16 into
-// xs[r * stride + c] and FP32 sums of each 32-column sub-block into Xs[r * xstride + c / 32].
+// xs[r * stride + c] and FP32 sums of each XG-column group (16 or 32) into Xs[r * xstride + c / XG].
 // The wave's first XB 16-byte loads per lane are issued before `after()` (the weight loads),
 // so waiting for them does not wait for the weights; later batches, if any, come after.
-template <int ACT, int XB, class After>
+template <int ACT, int XB, int XG, class After>
 __device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int ncols, _Float16 *xs,
                                                 int stride, float *Xs, int xstride, int lane,
                                                 After after) {
@@ -608,8 +612,8 @@ __device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int 
             }
             // lanes 4q..4q+3 hold the four 8-element chunks of one 32-element sub-block
             part += __shfl_xor(part, 1);
-            part += __shfl_xor(part, 2);
-            if (i < total && (c8 & 3) == 0) Xs[r * xstride + (c8 >> 2)] = part;
+            if (XG == 32) part += __shfl_xor(part, 2);
+            if (i < total && (c8 & (XG / 8 - 1)) == 0) Xs[r * xstride + c8 / (XG / 8)] = part;
         }
     }
     if (!issued) after();
@@ -685,30 +689,99 @@ __device__ __forceinline__ void q4k_block_fast(const Q4KItem &cur, const _Float1
     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[ul * 8 + 4 + g], cB, acc, 0, 0, 0);
 }
 
-// Small-row Q4_K kernel, one workgroup per TW consecutive 16-row tiles. Wave w of W owns blocks
-// [w U / W, (w+1) U / W) (U = K / 256) of every tile of the workgroup: it issues its activation
-// loads, then its first P (tile, block) items, stages its own activation columns in a private LDS
+// Q4_K as a small-row format: item = one 256-element block of a 16-row tile.
+struct GQ4K {
+    static constexpr int KU = 256;  // K per item
+    static constexpr int XG = 32;   // activation sum group
+    typedef Q4KItem Item;
+    struct Lane {
+        uint32_t sh;
+        float kfac;
+    };
+    __device__ static Lane lane_consts(int g) {
+        return Lane{8u * (uint32_t)g, (g & 1) ? -64.f : -1024.f};
+    }
+    __device__ static void load(Item &it, const QmmParams &p, int tile, int u, int g, int r) {
+        q4k_item_load(it, p.wq, p.K, tile, u, g, r);
+    }
+    template <int MV>
+    __device__ static void block(const Item &it, const _Float16 *xrow, const float *Xrow, int ul,
+                                 int g, const Lane &c, f32x4 &acc) {
+        q4k_block_fast<MV>(it, xrow, Xrow, ul, g, c.sh, c.kfac, acc);
+    }
+};
+
+// Q8_0 as a small-row format: item = 64 k (two blocks) of a 16-row tile. Block b is one MFMA on
+// the exact FP16 operands 1152 + q (0x6400 | (q + 128), the stored byte), scaled by d_b; the
+// 1152 X_b terms come from one FP32 MFMA 16x16x4 with lane groups 0, 1 holding blocks 0, 1
+// and groups 2, 3 zeros. This equals quant.rs:75-80's weights times x up to FP32 rounding.
+struct GQ8_0 {
+    static constexpr int KU = 64;
+    static constexpr int XG = 32;
+    struct Item {
+        uint4 q;
+        uint32_t d2;
+    };
+    struct Lane {};
+    __device__ static Lane lane_consts(int) { return Lane{}; }
+    __device__ static void load(Item &it, const QmmParams &p, int tile, int u, int g, int r) {
+        const uint8_t *tb = p.wq + ((size_t)tile * (size_t)(p.K / 64) + (size_t)u) * 1088u;
+        it.q = ld16(tb + (16 * g + r) * 16);
+        it.d2 = *(const uint32_t *)(tb + 1024 + 4 * r);
+    }
+    template <int MV>
+    __device__ static void block(const Item &it, const _Float16 *xrow, const float *Xrow, int ul,
+                                 int g, const Lane &, f32x4 &acc) {
+        const float d0 = h2f(it.d2), d1 = h2f(it.d2 >> 16);
+        uint32_t magic = 0x64006400u;
+        asm("" : "+v"(magic));
+        const uint32_t w[4] = {it.q.x, it.q.y, it.q.z, it.q.w};
+        f32x4 S[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            uint4 bq;
+            bq.x = (w[2 * b] & 0x00ff00ffu) | magic;
+            bq.y = ((w[2 * b] >> 8) & 0x00ff00ffu) | magic;
+            bq.z = (w[2 * b + 1] & 0x00ff00ffu) | magic;
+            bq.w = ((w[2 * b + 1] >> 8) & 0x00ff00ffu) | magic;
+            S[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xrow + ul * 64 + 32 * b + 8 * g),
+                                                          __builtin_bit_cast(f16x8, bq),
+                                                          f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < MV; ++i) {
+            acc[i] = __builtin_fmaf(d0, S[0][i], acc[i]);
+            acc[i] = __builtin_fmaf(d1, S[1][i], acc[i]);
+        }
+        const float cb = g >= 2 ? 0.f : -1152.f * (g ? d1 : d0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[ul * 2 + (g & 1)], cb, acc, 0, 0, 0);
+    }
+};
+
+// Small-row kernel, one workgroup per TW consecutive 16-row tiles. Wave w of W owns items
+// [w U / W, (w+1) U / W) (U = K / G::KU) of every tile of the workgroup: it issues its activation
+// loads, then its first P (tile, item) loads, stages its own activation columns in a private LDS
 // region (no workgroup barrier), and runs the items as they arrive, tile-major, refilling P
 // items ahead when they do not all fit. A wave's partial sum of each tile goes to its own LDS
 // region; after one barrier, wave t adds tile t's W partials in wave order. Each output element
 // is the same sum for every M and TW. Many short workgroups keep every compute unit fed as the
 // memory system serves them unevenly.
-template <int W, int TW, int P, int MV, int XB>
-__device__ __forceinline__ void qmv_q4k_body(const QmmParams &p) {
+template <class G, int W, int TW, int P, int MV, int XB>
+__device__ __forceinline__ void qmv_body(const QmmParams &p) {
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4;
     const int r16 = lane & 15;
-    const int U = p.K >> 8;
+    const int U = p.K / G::KU;
     const int T = p.N >> 4;
     const int tile0 = blockIdx.x * TW;
     const int ntw = min(TW, T - tile0);  // tiles of this workgroup (>= 1)
     const int u0 = wave * U / W;
     const int nu = (wave + 1) * U / W - u0;
     const int umax = (U + W - 1) / W;
-    const int stride = umax * 256 + kLdsPad;
-    const int xstride = umax * 8;
+    const int stride = umax * G::KU + kLdsPad;
+    const int xstride = umax * (G::KU / G::XG);
     // per wave: FP16 activations [M][stride], then sums [M][xstride]; reused for the partials
     const int region = max((p.M * stride * 2 + p.M * xstride * 4 + 15) & ~15, TW * 1024);  // bytes
     uint8_t *mine = (uint8_t *)lds + (size_t)wave * region;
@@ -716,26 +789,27 @@ __device__ __forceinline__ void qmv_q4k_body(const QmmParams &p) {
     float *Xs = (float *)(mine + p.M * stride * 2);
     const int nitems = nu * ntw;
 
-    auto load_item = [&](Q4KItem &dst, int idx) {
+    auto load_item = [&](typename G::Item &dst, int idx) {
         idx = min(idx, nitems - 1);
         const int tw = idx / nu;
-        q4k_item_load(dst, p.wq, p.K, tile0 + tw, u0 + (idx - tw * nu), g, r16);
+        G::load(dst, p, tile0 + tw, u0 + (idx - tw * nu), g, r16);
     };
     f32x4 acc[TW];
 #pragma unroll
     for (int t = 0; t < TW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (nu > 0) {
-        Q4KItem buf[P];
+        typename G::Item buf[P];
         auto issue = [&] {
 #pragma unroll
             for (int j = 0; j < P; ++j) load_item(buf[j], j);
         };
+        const int c0 = u0 * G::KU, nc = nu * G::KU;
         if (p.act == 0)
-            stage_wave_cols<0, XB>(p, u0 * 256, nu * 256, xs, stride, Xs, xstride, lane, issue);
+            stage_wave_cols<0, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
         else if (p.act == 1)
-            stage_wave_cols<1, XB>(p, u0 * 256, nu * 256, xs, stride, Xs, xstride, lane, issue);
+            stage_wave_cols<1, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
         else
-            stage_wave_cols<2, XB>(p, u0 * 256, nu * 256, xs, stride, Xs, xstride, lane, issue);
+            stage_wave_cols<2, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
         // LDS operations of one wave complete in order; this keeps the compiler from moving
         // the fragment reads above the staging writes.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -743,8 +817,7 @@ __device__ __forceinline__ void qmv_q4k_body(const QmmParams &p) {
         const int arow = min(r16, p.M - 1);  // rows >= M feed output rows that are never stored
         const _Float16 *xrow = xs + arow * stride;
         const float *Xrow = Xs + arow * xstride;
-        const uint32_t sh = 8u * (uint32_t)g;
-        const float kfac = (g & 1) ? -64.f : -1024.f;
+        const typename G::Lane lc = G::lane_consts(g);
         for (int i0 = 0; i0 < nitems; i0 += P) {
 #pragma unroll
             for (int j = 0; j < P; ++j) {
@@ -755,7 +828,7 @@ __device__ __forceinline__ void qmv_q4k_body(const QmmParams &p) {
 #pragma unroll
                     for (int t = 1; t < TW; ++t)
                         if (t == tw) a = acc[t];
-                    q4k_block_fast<MV>(buf[j], xrow, Xrow, idx - tw * nu, g, sh, kfac, a);
+                    G::template block<MV>(buf[j], xrow, Xrow, idx - tw * nu, g, lc, a);
 #pragma unroll
                     for (int t = 0; t < TW; ++t)
                         if (t == tw) acc[t] = a;
@@ -800,13 +873,24 @@ __device__ __forceinline__ void qmv_q4k_body(const QmmParams &p) {
 #define JV_QMV(TW, MV, XB)                                                                   \
     extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(TW == 1 ? 8 : 4))) \
     void jv_qmv_q4k_t##TW##_m##MV(QmmParams p) {                                             \
-        qmv_q4k_body<8, TW, 2 * TW, MV, XB>(p);                                             \
+        qmv_body<GQ4K, 8, TW, 2 * TW, MV, XB>(p);                                            \
     }
 JV_QMV(1, 1, 2)
 JV_QMV(1, 2, 4)
 JV_QMV(2, 1, 4)
 JV_QMV(2, 2, 4)
 JV_QMV(2, 4, 8)
+
+// Q8_0: 16 waves, each four 64-k items of a tile at K = 4096 (all in flight).
+#define JV_QMV8(TW, MV, XB)                                                                  \
+    extern "C" __global__ __launch_bounds__(1024) void jv_qmv_q8_0_t##TW##_m##MV(QmmParams p) { \
+        qmv_body<GQ8_0, 16, TW, 4 * TW, MV, XB>(p);                                          \
+    }
+JV_QMV8(1, 1, 2)
+JV_QMV8(1, 2, 4)
+JV_QMV8(2, 1, 4)
+JV_QMV8(2, 2, 4)
+JV_QMV8(2, 4, 8)
 
 // ---------------------------------------------------------------------------------------------
 // Entry points (looked up by name with hipModuleGetFunction).
@@ -1213,21 +1297,25 @@ extern "C" __global__ __launch_bounds__(256) void jv_repack_q6k(RepackParams p) 
 }
 
 // One work item per pair of Q8_0 blocks (64 k of one row).
-extern "C" __global__ __launch_bounds__(256) void jv_repack_q8_0(RepackParams p) {
-    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+// One work item per 64 k of a row (two Q8_0 blocks): 68 raw bytes -> its pieces of the tile layout.
+extern "C" __global__ __launch_bounds__(256) void jv_repack_q8_0(RepackParams p, int32_t kchunks) {
+    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;  // row * kchunks + u
     if (c >= p.chunks) return;
+    const int64_t row = c / kchunks;
+    const int64_t u = c - row * kchunks;
+    const int rr = (int)(row & 15);
     const uint8_t *src = p.raw + c * 68;
-    uint8_t *dst = p.wq + c * 64;
+    uint8_t *tb = p.wq + ((row >> 4) * kchunks + u) * 1088;
+    const int order[8] = {0, 2, 1, 3, 4, 6, 5, 7};
     for (int g = 0; g < 4; ++g)
         for (int blk = 0; blk < 2; ++blk)
-            for (int e = 0; e < 8; ++e) dst[16 * g + 8 * blk + e] = src[34 * blk + 2 + 8 * g + e];
+            for (int e = 0; e < 8; ++e)
+                tb[(16 * g + rr) * 16 + 8 * blk + e] = (uint8_t)(src[34 * blk + 2 + 8 * g + order[e]] ^ 0x80u);
     for (int blk = 0; blk < 2; ++blk) {
-        p.wd[4 * c + 2 * blk] = src[34 * blk];
-        p.wd[4 * c + 2 * blk + 1] = src[34 * blk + 1];
+        tb[1024 + 4 * rr + 2 * blk] = src[34 * blk];
+        tb[1024 + 4 * rr + 2 * blk + 1] = src[34 * blk + 1];
     }
 }
-
-// One work item per pair of Q5_0 blocks (64 k of one row).
 extern "C" __global__ __launch_bounds__(256) void jv_repack_q5_0(RepackParams p) {
     const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (c >= p.chunks) return;
