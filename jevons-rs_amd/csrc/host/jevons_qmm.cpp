@@ -202,7 +202,7 @@ Layout layout_for(jv_fmt fmt, size_t blocks) {
     Layout l;
     switch (fmt) {
     case JV_FMT_Q4K: l.q = blocks * 144; break;
-    case JV_FMT_Q6K: l.q = blocks * 208; l.d = blocks * 2; break;
+    case JV_FMT_Q6K: l.q = blocks * 210; break;
     case JV_FMT_Q8_0: l.q = blocks * 34; break;
     case JV_FMT_Q5_0: l.q = blocks * 16; l.h = blocks * 4; l.d = blocks * 2; break;
     default: break;
@@ -288,6 +288,8 @@ jv_status build_from_device(jv_ctx *ctx, uint32_t type, jv_fmt fmt, size_t n, si
         if (fmt == JV_FMT_Q6K) {
             rp.chunks = (int64_t)blocks;
             name = "jv_repack_q6k";
+            kchunks = (int32_t)(k / 256);
+            args[1] = &kchunks;
         } else if (fmt == JV_FMT_Q8_0) {
             rp.chunks = (int64_t)(blocks / 2);
             name = "jv_repack_q8_0";
@@ -346,23 +348,34 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
     if (!x || !out) return fail(JV_ERR_INVALID, "null activation or output buffer");
     if (((uintptr_t)x & 15u) != 0) return fail(JV_ERR_INVALID, "activations must be 16-byte aligned");
 
-    // Small-row Q4_K and Q8_0 kernels: one workgroup per one or two 16-row tiles (two from m = 3
-    // on, which halves the activation staging per weight byte); both sum each output element the
+    // Small-row Q4_K, Q6_K and Q8_0 kernels. Up to 8 tiles (16 rows) per compute unit: one
+    // workgroup per one or two tiles (two from m = 3 on for Q4_K and Q8_0, which halves the
+    // activation staging per weight byte). Wider matrices: persistent workgroups that stage the
+    // activations once and stream a range of tiles. All variants sum each output element the
     // same way, so every output row is the same for any m.
-    if (plan.bm == 0 && (w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q8_0) &&
+    if (plan.bm == 0 && (w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
         w->n * w->experts * w->k < (1ull << 32)) {
-        const bool q4k = w->fmt == JV_FMT_Q4K;
-        const int tw = m <= 2 ? 1 : 2;
-        const int waves = q4k ? 8 : 16;
-        const int ku = q4k ? 256 : 64;  // K per item; activation sums per 32 columns
+        const bool q8 = w->fmt == JV_FMT_Q8_0, q6 = w->fmt == JV_FMT_Q6K;
+        const char *fname = q8 ? "q8_0" : (q6 ? "q6k" : "q4k");
+        const int mv = m == 1 ? 1 : (m == 2 ? 2 : 4);
+        const int cus = std::max(1, ctx->info.compute_units);
+        const int waves = q8 ? 16 : 8;
+        const int ku = q8 ? 64 : 256;  // K per item
+        const int xg = q6 ? 16 : 32;   // columns per activation sum
         const int U = (int)(w->k / ku);
         const int T = (int)(w->n * w->experts / 16);
         const int umax = (U + waves - 1) / waves;
-        // per wave: FP16 activations [m][ku umax + 8] and sums [m][ku umax / 32], then the wave's
-        // tile partials (tw KB); qmv_body computes the same size
-        const size_t stage = ((size_t)m * ((size_t)umax * ku + 8) * 2 + (size_t)m * umax * (ku / 32) * 4 + 15) &
+        const bool persist = T >= 8 * cus;
+        const int tw = persist || q6 || m <= 2 ? 1 : 2;
+        // per wave: FP16 activations [m][ku umax + 8], sums [m][ku umax / xg] and, for Q6_K, a
+        // zero row [ku umax + 8]. The per-tile kernels reuse it for the wave's tile partials
+        // (tw KB); the persistent ones add two chunks of 2 tiles x waves partials. The kernels
+        // compute the same sizes.
+        const size_t row = ((size_t)umax * ku + 8) * 2;
+        const size_t stage = ((size_t)m * row + (size_t)m * umax * (ku / xg) * 4 + (q6 ? row : 0) + 15) &
                              ~(size_t)15;
-        const size_t lds = std::max(stage, (size_t)tw * 1024) * waves;
+        const size_t lds = persist ? stage * waves + 2 * 2 * (size_t)waves * 1024
+                                   : std::max(stage, (size_t)tw * 1024) * waves;
         if (lds <= ctx->info.lds_bytes) {
             QmmParams p{};
             p.x = x;
@@ -378,8 +391,17 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
             p.splits = 1;
             void *args[] = {&p};
             char name[32];
-            snprintf(name, sizeof name, "jv_qmv_%s_t%d_m%d", q4k ? "q4k" : "q8_0", tw,
-                     m == 1 ? 1 : (m == 2 ? 2 : 4));
+            if (persist) {
+                snprintf(name, sizeof name, "jv_qmvp_%s_m%d", fname, mv);
+                hipFunction_t f;
+                st = get_fn(ctx, name, &f);
+                if (st != JV_OK) return st;
+                int per_cu = 0;
+                JV_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 64 * waves, lds));
+                const int grid = std::min(T, cus * std::max(1, per_cu));
+                return launch(ctx, name, dim3((unsigned)grid), dim3(64 * waves), lds, stream, args);
+            }
+            snprintf(name, sizeof name, "jv_qmv_%s_t%d_m%d", fname, tw, mv);
             return launch(ctx, name, dim3((unsigned)((T + tw - 1) / tw)), dim3(64 * waves), lds, stream, args);
         }
     }

@@ -161,11 +161,12 @@ struct FQ4K {
     }
 };
 
-// Q6_K, device layout: per block 208 bytes + one FP16 scale in the d region.
-// Bytes 48g..48g+47 hold lane group g's quants: ql(hf, i2) = ql[64hf + 32i2 + 8g, +8) for
-// (hf, i2) = (0,0), (0,1), (1,0), (1,1), then qh(hf) = qh[32hf + 8g, +8) for hf = 0, 1;
-// bytes 192..207 are the 16 int8 sub-block scales. Step s = 4hf + i covers elements
-// 128hf + 32i + 8g + e (quant.rs:43-61).
+// Q6_K, device layout: 16-row tiles, per 256 k 3360 bytes. Lane 16g + r owns 48 bytes of row r,
+// in three 16-byte pieces at [0, 1024), [1024, 2048), [2048, 3072) (piece i at 1024 i + 16 lane):
+// ql(hf, i2) = ql[64hf + 32i2 + 8g, +8) for (hf, i2) = (0,0), (0,1), (1,0), (1,1), then
+// qh(hf) = qh[32hf + 8g, +8) for hf = 0, 1, each 4-byte group stored in the order {0, 2, 1, 3};
+// [3072, 3328) the rows' 16 int8 scales (16 bytes per row), [3328, 3360) their FP16 d.
+// Step s = 4hf + i covers elements 128hf + 32i + 8g + e (quant.rs:43-61).
 struct FQ6K {
     static constexpr int KU = 256;
     struct Raw {
@@ -175,15 +176,15 @@ struct FQ6K {
     struct Prep {
         float d;
     };
-    __device__ static void load(Raw &r, const uint8_t *wq, const uint8_t *, const uint8_t *wd,
+    __device__ static void load(Raw &r, const uint8_t *wq, const uint8_t *, const uint8_t *,
                                 int K, int row, int u, int g) {
-        const size_t blk_i = (size_t)row * (size_t)(K / 256) + (size_t)u;
-        const uint8_t *blk = wq + blk_i * 208u;
-        r.a = ld16(blk + 48 * g);
-        r.b = ld16(blk + 48 * g + 16);
-        r.c = ld16(blk + 48 * g + 32);
-        r.sc = ld16(blk + 192);
-        r.d = *(const uint16_t *)(wd + blk_i * 2u);
+        const uint8_t *tb = wq + ((size_t)(row >> 4) * (size_t)(K / 256) + (size_t)u) * 3360u;
+        const int rr = row & 15, lo = (16 * g + rr) * 16;
+        r.a = ld16(tb + lo);
+        r.b = ld16(tb + 1024 + lo);
+        r.c = ld16(tb + 2048 + lo);
+        r.sc = ld16(tb + 3072 + 16 * rr);
+        r.d = *(const uint16_t *)(tb + 3328 + 2 * rr);
     }
     __device__ static void prep(const Raw &r, Prep &p, int) { p.d = h2f(r.d); }
     __device__ static int kidx(int s, int g) { return 32 * s + 8 * g; }
@@ -200,8 +201,9 @@ struct FQ6K {
         const float scale = p.d * (float)sc;  // exact: 11 x 8 significant bits
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const uint32_t ql = w[qi + (e >> 2)] >> (8 * (e & 3) + nib);
-            const uint32_t qh = w[hi + (e >> 2)] >> (8 * (e & 3) + 2 * i);
+            const int pos = ((e & 1) << 1) | ((e >> 1) & 1);  // stored byte of element e & 3
+            const uint32_t ql = w[qi + (e >> 2)] >> (8 * pos + nib);
+            const uint32_t qh = w[hi + (e >> 2)] >> (8 * pos + 2 * i);
             const int32_t q = (int32_t)((ql & 15u) | ((qh & 3u) << 4)) - 32;
             v[e] = scale * (float)q;  // (d * sc) * q, as quant.rs evaluates it
         }
@@ -693,6 +695,7 @@ __device__ __forceinline__ void q4k_block_fast(const Q4KItem &cur, const _Float1
 struct GQ4K {
     static constexpr int KU = 256;  // K per item
     static constexpr int XG = 32;   // activation sum group
+    static constexpr bool kZeroRow = false;
     typedef Q4KItem Item;
     struct Lane {
         uint32_t sh;
@@ -705,8 +708,8 @@ struct GQ4K {
         q4k_item_load(it, p.wq, p.K, tile, u, g, r);
     }
     template <int MV>
-    __device__ static void block(const Item &it, const _Float16 *xrow, const float *Xrow, int ul,
-                                 int g, const Lane &c, f32x4 &acc) {
+    __device__ static void block(const Item &it, const _Float16 *xrow, const _Float16 *, const float *Xrow,
+                                 int ul, int g, const Lane &c, f32x4 &acc) {
         q4k_block_fast<MV>(it, xrow, Xrow, ul, g, c.sh, c.kfac, acc);
     }
 };
@@ -718,6 +721,7 @@ struct GQ4K {
 struct GQ8_0 {
     static constexpr int KU = 64;
     static constexpr int XG = 32;
+    static constexpr bool kZeroRow = false;
     struct Item {
         uint4 q;
         uint32_t d2;
@@ -730,8 +734,8 @@ struct GQ8_0 {
         it.d2 = *(const uint32_t *)(tb + 1024 + 4 * r);
     }
     template <int MV>
-    __device__ static void block(const Item &it, const _Float16 *xrow, const float *Xrow, int ul,
-                                 int g, const Lane &, f32x4 &acc) {
+    __device__ static void block(const Item &it, const _Float16 *xrow, const _Float16 *, const float *Xrow,
+                                 int ul, int g, const Lane &, f32x4 &acc) {
         const float d0 = h2f(it.d2), d1 = h2f(it.d2 >> 16);
         uint32_t magic = 0x64006400u;
         asm("" : "+v"(magic));
@@ -755,6 +759,85 @@ struct GQ8_0 {
         }
         const float cb = g >= 2 ? 0.f : -1152.f * (g ? d1 : d0);
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[ul * 2 + (g & 1)], cb, acc, 0, 0, 0);
+    }
+};
+
+// Q6_K as a small-row format: item = one 256-element block of a 16-row tile. Step s (32 k,
+// lane group g holding k = 32s + 8g + e) builds the exact FP16 operands 1024 + q6 from the low
+// nibble and the two high bits, and runs two MFMAs on them: one with the activations of lane
+// groups 0, 1 (scale group 2s) and one with those of groups 2, 3 (group 2s + 1), the other
+// half reading a zero row. Then out += d sum_t sc_t S_t - sum_t 1056 d sc_t X_t (1056 = 1024
+// + the 32 offset of quant.rs:43-61's q - 32), the second sum as four FP32 MFMAs 16x16x4 over
+// the 16-column activation sums (k index g: group 4j + g).
+struct GQ6K {
+    static constexpr int KU = 256;
+    static constexpr int XG = 16;
+    static constexpr bool kZeroRow = true;
+    struct Item {
+        uint4 a, b, c;
+        uint32_t hv;  // scale bytes 4g .. 4g + 3 of row r
+        uint32_t dv;  // FP16 d of row r
+    };
+    struct Lane {
+        uint32_t sh;
+    };
+    __device__ static Lane lane_consts(int g) { return Lane{8u * (uint32_t)g}; }
+    __device__ static void load(Item &it, const QmmParams &p, int tile, int u, int g, int r) {
+        const uint8_t *tb = p.wq + ((size_t)tile * (size_t)(p.K / 256) + (size_t)u) * 3360u;
+        const uint32_t lo = (uint32_t)(16 * g + r) * 16u;
+        it.a = ld16(tb + lo);
+        it.b = ld16(tb + 1024u + lo);
+        it.c = ld16(tb + 2048u + lo);
+        it.hv = *(const uint32_t *)(tb + 3072u + (uint32_t)(16 * r + 4 * g));
+        it.dv = *(const uint16_t *)(tb + 3328u + (uint32_t)(2 * r));
+    }
+    template <int MV>
+    __device__ static void block(const Item &it, const _Float16 *xrow, const _Float16 *zrow,
+                                 const float *Xrow, int ul, int g, const Lane &c, f32x4 &acc) {
+        const uint4 scw = q4k_head_gather(it.hv);  // the row's 16 scales, 4 per dword
+        const uint32_t SC[4] = {scw.x, scw.y, scw.z, scw.w};
+        const float d = h2f(it.dv);
+        const uint32_t W[12] = {it.a.x, it.a.y, it.a.z, it.a.w, it.b.x, it.b.y,
+                                it.b.z, it.b.w, it.c.x, it.c.y, it.c.z, it.c.w};
+        uint32_t magic = 0x64006400u;
+        asm("" : "+v"(magic));
+        const int kb = ul * 256 + 8 * g;
+        const _Float16 *xlo = (g < 2 ? xrow : zrow) + kb;
+        const _Float16 *xhi = (g < 2 ? zrow : xrow) + kb;
+        float v[MV];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const int hf = s >> 2, i = s & 3;
+            const int qi = 2 * (2 * hf + (i & 1)), nib = 4 * (i >> 1);
+            u32x4 bq;
+#pragma unroll
+            for (int pr = 0; pr < 4; ++pr) {
+                const uint32_t L = W[qi + (pr >> 1)] >> (8 * (pr & 1) + nib);
+                const uint32_t H = W[8 + 2 * hf + (pr >> 1)] >> (8 * (pr & 1) + 2 * i);
+                bq[pr] = (L & 0x000f000fu) | ((H & 0x00030003u) << 4) | magic;
+            }
+            const f16x8 bf = __builtin_bit_cast(f16x8, bq);
+            const f32x4 S0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xlo + 32 * s), bf,
+                                                                    f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            const f32x4 S1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xhi + 32 * s), bf,
+                                                                    f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            const int t0 = 2 * s, t1 = 2 * s + 1;
+            const float sc0 = (float)(int32_t)(int8_t)((SC[t0 >> 2] >> (8 * (t0 & 3))) & 0xffu);
+            const float sc1 = (float)(int32_t)(int8_t)((SC[t1 >> 2] >> (8 * (t1 & 3))) & 0xffu);
+#pragma unroll
+            for (int m = 0; m < MV; ++m) {
+                v[m] = s == 0 ? sc0 * S0[m] : __builtin_fmaf(sc0, S0[m], v[m]);
+                v[m] = __builtin_fmaf(sc1, S1[m], v[m]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MV; ++m) acc[m] = __builtin_fmaf(d, v[m], acc[m]);
+        const float kd = -1056.f * d;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float sc = (float)(int32_t)(int8_t)((SC[j] >> c.sh) & 0xffu);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[ul * 16 + 4 * j + g], kd * sc, acc, 0, 0, 0);
+        }
     }
 };
 
@@ -782,11 +865,14 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p) {
     const int umax = (U + W - 1) / W;
     const int stride = umax * G::KU + kLdsPad;
     const int xstride = umax * (G::KU / G::XG);
-    // per wave: FP16 activations [M][stride], then sums [M][xstride]; reused for the partials
-    const int region = max((p.M * stride * 2 + p.M * xstride * 4 + 15) & ~15, TW * 1024);  // bytes
+    // per wave: FP16 activations [M][stride], sums [M][xstride], and for formats that mask
+    // activation fragments a zero row [stride]; reused for the partials
+    const int zbytes = G::kZeroRow ? stride * 2 : 0;
+    const int region = max((p.M * stride * 2 + p.M * xstride * 4 + zbytes + 15) & ~15, TW * 1024);  // bytes
     uint8_t *mine = (uint8_t *)lds + (size_t)wave * region;
     _Float16 *xs = (_Float16 *)mine;
     float *Xs = (float *)(mine + p.M * stride * 2);
+    _Float16 *zrow = (_Float16 *)(mine + p.M * stride * 2 + p.M * xstride * 4);
     const int nitems = nu * ntw;
 
     auto load_item = [&](typename G::Item &dst, int idx) {
@@ -804,6 +890,8 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p) {
             for (int j = 0; j < P; ++j) load_item(buf[j], j);
         };
         const int c0 = u0 * G::KU, nc = nu * G::KU;
+        if (G::kZeroRow)
+            for (int i = lane; i < stride / 8; i += 64) *(f16x8 *)(zrow + 8 * i) = f16x8{};
         if (p.act == 0)
             stage_wave_cols<0, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
         else if (p.act == 1)
@@ -828,7 +916,7 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p) {
 #pragma unroll
                     for (int t = 1; t < TW; ++t)
                         if (t == tw) a = acc[t];
-                    G::template block<MV>(buf[j], xrow, Xrow, idx - tw * nu, g, lc, a);
+                    G::template block<MV>(buf[j], xrow, zrow, Xrow, idx - tw * nu, g, lc, a);
 #pragma unroll
                     for (int t = 0; t < TW; ++t)
                         if (t == tw) acc[t] = a;
@@ -865,6 +953,123 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p) {
     }
 }
 
+// Persistent variant of qmv_body for wide matrices (many more tiles than compute units):
+// workgroup c owns tiles [c T / G, (c + 1) T / G) and stages its activation columns once. Each
+// wave runs its (tile, item) list tile-major with P loads in flight across tile boundaries and
+// writes its partial of every tile to an LDS slot; after every TS tiles one barrier, then wave t
+// adds tile t's W partials in wave order (slots double-buffered, so the next chunk's partials
+// never overwrite ones still being added). Every output element is the same sum as in qmv_body.
+template <class G, int W, int TS, int P, int MV, int XB>
+__device__ __forceinline__ void qmvp_body(const QmmParams &p) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4;
+    const int r16 = lane & 15;
+    const int U = p.K / G::KU;
+    const int T = p.N >> 4;
+    const int t_begin = (int)((int64_t)blockIdx.x * T / gridDim.x);
+    const int nt = (int)((int64_t)(blockIdx.x + 1) * T / gridDim.x) - t_begin;  // >= 1
+    const int u0 = wave * U / W;
+    const int nu = (wave + 1) * U / W - u0;
+    const int umax = (U + W - 1) / W;
+    const int stride = umax * G::KU + kLdsPad;
+    const int xstride = umax * (G::KU / G::XG);
+    const int zbytes = G::kZeroRow ? stride * 2 : 0;
+    const int region = (p.M * stride * 2 + p.M * xstride * 4 + zbytes + 15) & ~15;  // bytes
+    uint8_t *mine = (uint8_t *)lds + (size_t)wave * region;
+    _Float16 *xs = (_Float16 *)mine;
+    float *Xs = (float *)(mine + p.M * stride * 2);
+    _Float16 *zrow = (_Float16 *)(mine + p.M * stride * 2 + p.M * xstride * 4);
+    f32x4 *part = (f32x4 *)((uint8_t *)lds + (size_t)W * region);  // [2][TS][W][64]
+
+    int chunk = 0, tt = 0;
+    auto store = [&](int tile, const f32x4 &v) {
+        const int col = tile * 16 + r16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * g + i;
+            if (m < p.M) {
+                const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
+                if (p.out_type == 0)
+                    ((float *)p.out)[o] = v[i];
+                else
+                    ((uint16_t *)p.out)[o] = (uint16_t)f2bf(v[i]);
+            }
+        }
+    };
+    // this wave's partial of tile tt of the current chunk is `a`
+    auto end_tile = [&](const f32x4 &a) {
+        const int tc = min(TS, nt - chunk * TS);
+        part[(((chunk & 1) * TS + tt) * W + wave) * 64 + lane] = a;
+        if (++tt == tc) {
+            lds_barrier();
+            for (int t = wave; t < tc; t += W) {
+                const f32x4 *src = part + ((chunk & 1) * TS + t) * W * 64 + lane;
+                f32x4 sum = src[0];
+                for (int w = 1; w < W; ++w) {
+                    const f32x4 v = src[w * 64];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) sum[i] += v[i];
+                }
+                store(t_begin + chunk * TS + t, sum);
+            }
+            ++chunk;
+            tt = 0;
+        }
+    };
+
+    if (nu > 0) {
+        const int nitems = nu * nt;
+        int ld_t = 0, ld_u = 0;  // (tile, item) of the next load
+        auto load_next = [&](typename G::Item &dst) {
+            G::load(dst, p, t_begin + ld_t, u0 + ld_u, g, r16);
+            if (++ld_u == nu) {
+                ld_u = 0;
+                ld_t = min(ld_t + 1, nt - 1);  // past the end: reload the last tile (unused)
+            }
+        };
+        typename G::Item buf[P];
+        auto issue = [&] {
+#pragma unroll
+            for (int j = 0; j < P; ++j) load_next(buf[j]);
+        };
+        const int c0 = u0 * G::KU, nc = nu * G::KU;
+        if (G::kZeroRow)
+            for (int i = lane; i < stride / 8; i += 64) *(f16x8 *)(zrow + 8 * i) = f16x8{};
+        if (p.act == 0)
+            stage_wave_cols<0, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
+        else if (p.act == 1)
+            stage_wave_cols<1, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
+        else
+            stage_wave_cols<2, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+
+        const int arow = min(r16, p.M - 1);  // rows >= M feed output rows that are never stored
+        const _Float16 *xrow = xs + arow * stride;
+        const float *Xrow = Xs + arow * xstride;
+        const typename G::Lane lc = G::lane_consts(g);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        int ul = 0;
+        for (int i0 = 0; i0 < nitems; i0 += P) {
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                if (i0 + j < nitems) {
+                    G::template block<MV>(buf[j], xrow, zrow, Xrow, ul, g, lc, acc);
+                    if (++ul == nu) {
+                        end_tile(acc);
+                        acc = f32x4{0.f, 0.f, 0.f, 0.f};
+                        ul = 0;
+                    }
+                }
+                if (i0 + P < nitems) load_next(buf[j]);
+            }
+        }
+    } else {
+        for (int t = 0; t < nt; ++t) end_tile(f32x4{0.f, 0.f, 0.f, 0.f});
+    }
+}
+
 }  // namespace
 
 // One-tile workgroups run four per compute unit (8 waves per SIMD, at most 64 VGPRs); the
@@ -880,6 +1085,30 @@ JV_QMV(1, 2, 4)
 JV_QMV(2, 1, 4)
 JV_QMV(2, 2, 4)
 JV_QMV(2, 4, 8)
+
+// Q6_K: 8 waves, each two blocks of a tile at K = 3840 (all in flight); one tile per workgroup.
+#define JV_QMV6(TW, MV, XB)                                                                  \
+    extern "C" __global__ __launch_bounds__(512) void jv_qmv_q6k_t##TW##_m##MV(QmmParams p) { \
+        qmv_body<GQ6K, 8, TW, 2 * TW, MV, XB>(p);                                            \
+    }
+JV_QMV6(1, 1, 2)
+JV_QMV6(1, 2, 4)
+JV_QMV6(1, 4, 8)
+
+// Persistent kernels for wide matrices: chunks of two tiles, four items in flight per wave.
+#define JV_QMVP(NAME, G, W, MV, XB)                                                          \
+    extern "C" __global__ __launch_bounds__(64 * W) void jv_qmvp_##NAME##_m##MV(QmmParams p) { \
+        qmvp_body<G, W, 2, 4, MV, XB>(p);                                                    \
+    }
+JV_QMVP(q4k, GQ4K, 8, 1, 2)
+JV_QMVP(q4k, GQ4K, 8, 2, 4)
+JV_QMVP(q4k, GQ4K, 8, 4, 8)
+JV_QMVP(q6k, GQ6K, 8, 1, 2)
+JV_QMVP(q6k, GQ6K, 8, 2, 4)
+JV_QMVP(q6k, GQ6K, 8, 4, 8)
+JV_QMVP(q8_0, GQ8_0, 16, 1, 2)
+JV_QMVP(q8_0, GQ8_0, 16, 2, 4)
+JV_QMVP(q8_0, GQ8_0, 16, 4, 8)
 
 // Q8_0: 16 waves, each four 64-k items of a tile at K = 4096 (all in flight).
 #define JV_QMV8(TW, MV, XB)                                                                  \
@@ -1277,26 +1506,31 @@ extern "C" __global__ __launch_bounds__(256) void jv_repack_q4k(RepackParams p, 
     }
 }
 
-// One work item per Q6_K block: 210 raw bytes -> 208 layout bytes + FP16 scale.
-extern "C" __global__ __launch_bounds__(256) void jv_repack_q6k(RepackParams p) {
-    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+// One work item per Q6_K block row: 210 raw bytes -> its pieces of the tile layout.
+extern "C" __global__ __launch_bounds__(256) void jv_repack_q6k(RepackParams p, int32_t kblocks) {
+    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;  // row * kblocks + u
     if (b >= p.chunks) return;
+    const int64_t row = b / kblocks;
+    const int64_t u = b - row * kblocks;
+    const int rr = (int)(row & 15);
     const uint8_t *src = p.raw + b * 210;
-    uint8_t *dst = p.wq + b * 208;
+    uint8_t *tb = p.wq + ((row >> 4) * kblocks + u) * 3360;
+    const int order[4] = {0, 2, 1, 3};
     for (int g = 0; g < 4; ++g) {
-        uint8_t *o = dst + 48 * g;
+        uint8_t o[48];
         for (int hf = 0; hf < 2; ++hf)
             for (int i2 = 0; i2 < 2; ++i2)
                 for (int e = 0; e < 8; ++e) o[8 * (2 * hf + i2) + e] = src[64 * hf + 32 * i2 + 8 * g + e];
         for (int hf = 0; hf < 2; ++hf)
             for (int e = 0; e < 8; ++e) o[32 + 8 * hf + e] = src[128 + 32 * hf + 8 * g + e];
+        for (int piece = 0; piece < 3; ++piece)
+            for (int e = 0; e < 16; ++e)
+                tb[1024 * piece + (16 * g + rr) * 16 + e] = o[16 * piece + (e & ~3) + order[e & 3]];
     }
-    for (int e = 0; e < 16; ++e) dst[192 + e] = src[192 + e];
-    p.wd[2 * b] = src[208];
-    p.wd[2 * b + 1] = src[209];
+    for (int e = 0; e < 16; ++e) tb[3072 + 16 * rr + e] = src[192 + e];
+    tb[3328 + 2 * rr] = src[208];
+    tb[3328 + 2 * rr + 1] = src[209];
 }
-
-// One work item per pair of Q8_0 blocks (64 k of one row).
 // One work item per 64 k of a row (two Q8_0 blocks): 68 raw bytes -> its pieces of the tile layout.
 extern "C" __global__ __launch_bounds__(256) void jv_repack_q8_0(RepackParams p, int32_t kchunks) {
     const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;  // row * kchunks + u

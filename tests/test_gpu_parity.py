@@ -155,6 +155,40 @@ def test_every_plan_matches_oracle_and_tiles_are_row_invariant(gpu, name, type_i
     assert np.array_equal(gemv_rows[3], gemv_rows[16][:3])
 
 
+@pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0)])
+def test_small_row_product_of_wide_matrices(gpu, name, type_id):
+    """Matrices with at least 8 tiles of 16 rows per compute unit take the persistent small-row
+    kernels (activations staged once per workgroup, a range of tiles each): every output against
+    the f64 oracle, every row independent of m, and a row of the wide matrix equal to the same
+    weight row in a narrow matrix (the per-tile kernels)."""
+    cus = gpu.info.compute_units
+    n = 64 * (2 * cus + 1)  # 8 tiles per compute unit and 4 more: not a multiple of the grid
+    k = 512
+    w, raw = make_matrix(gpu, type_id, n, k, seed=11)
+    x_all = synth.normal_rows(60, 16, k)
+    rows = {}
+    for m in (1, 2, 5, 16):
+        x, xv = activations("bf16", x_all[:m])
+        say(name, "wide", n, k, "m", m)
+        out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matmul(gpu, x, m, w, out, jq.SplitScratch(gpu))
+        got = out.cpu().numpy()
+        e = err(got, oracle_product(type_id, raw, n, k, xv))
+        assert e <= TOL, f"m={m}: normalized error {e:.2e}"
+        rows[m] = got
+    assert np.array_equal(rows[1], rows[2][:1])
+    assert np.array_equal(rows[2], rows[5][:2])
+    assert np.array_equal(rows[5], rows[16][:5])
+    # the first 64 weight rows as a matrix of their own run on the per-tile kernels
+    per_row = {jq.Q4K: 144 * k // 256, jq.Q6K: 210 * k // 256, jq.Q8_0: 34 * k // 32}[type_id]
+    narrow, _ = make_matrix(gpu, type_id, 64, k, seed=0, raw=raw[:64 * per_row].copy())
+    for m in (1, 5):
+        x, _ = activations("bf16", x_all[:m])
+        out = torch.empty((m, 64), dtype=torch.float32, device="cuda")
+        jq.matmul(gpu, x, m, narrow, out, jq.SplitScratch(gpu))
+        assert np.array_equal(out.cpu().numpy(), rows[m][:, :64]), m
+
+
 def test_reference_dense_plan_recipe(gpu):
     """every_tunable_dense_plan_matches_reference_and_tiles_are_row_invariant
     (gpu/tests.rs:427-480): Q8_0 N=256 K=512, FP16 rows, every reference plan."""
