@@ -4,7 +4,8 @@ Step = one Q4_K decode GEMV at M = 1, 4 and 8 (K = 3840, N = 15360, bf16 activat
 out), each on a different copy of the weights: the copies rotate through more than 512 MiB so the
 256 MiB last-level cache cannot serve them. `value` is the weight bytes of the timed steps over
 their wall time (HIP graph replay, inputs resident in HBM). The Q4_K prefill GEMM (M = 512, 1%
-outlier columns) is timed the same way and reported under "gemm".
+outlier columns) is timed the same way and reported under "gemm"; the Q8_0 GEMV, the six layer
+GEMMs at M = 256 and the Q6_K vocabulary projection with its argmax under "configs".
 
 Roofline entries use each kernel's average launch duration: one HIP graph of R back-to-back
 launches per kernel, replayed between two events recorded on the stream the graph runs on,
@@ -18,7 +19,7 @@ HBM traffic: two rocprofv3 --pmc passes over a short run of the same launches (F
 WRITE_SIZE, KiB per dispatch), each scaled by what the counter reads in the same pass for a
 device-to-device copy of the same byte count, whose traffic is known.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-traffic]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-traffic] [--no-configs]
 """
 from __future__ import annotations
 
@@ -181,6 +182,94 @@ def measure_traffic(wbytes):
         shutil.rmtree(workdir, ignore_errors=True)
 
 
+def measure_configs(gpu, steps):
+    """Kernel durations of the other product configurations, each against its roofline:
+    Q8_0 GEMV (M=1, K=N=4096; weights rotated), the six layer GEMMs of one transformer block at
+    M=256 (Q4_K q/k/v/o/gate_up, Q6_K down), and the Q6_K vocabulary projection (K=3840,
+    N=262144, M = 1, 8, 32) with the per-row argmax of its logits."""
+    import numpy as np
+    import torch
+
+    import jevons_qmm as jq
+    from jevons_qmm import synth
+
+    def mats(kind, n, k, copies, seed):
+        raw = synth.weights(kind, seed, n, k)
+        dev = torch.from_numpy(raw).cuda()
+        ms = [jq.QMatrix.upload_device(gpu, kind, n, k, 1, dev) for _ in range(copies)]
+        del dev
+        return ms, raw.size
+
+    def xrows(m, k, seed):
+        xb = synth.to_bf16(synth.normal_rows(seed, m, k)).view(np.int16).copy()
+        return torch.from_numpy(xb).view(torch.bfloat16).cuda()
+
+    scratch = jq.SplitScratch(gpu)
+    res = {}
+    # Q8_0 GEMV
+    n, k = 4096, 4096
+    ms, wbytes = mats(jq.Q8_0, n, k, max(2, math.ceil(ROTATION_BYTES / (n * k // 32 * 34))), 3)
+    x = xrows(1, k, 1)
+    out = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    jq.matmul(gpu, x, 1, ms[0], out, scratch)  # buffers grow outside graph capture
+    t = kernel_time_ms(lambda r: jq.matmul(gpu, x, 1, ms[r % len(ms)], out, scratch), steps)
+    gbs = wbytes / (t * 1e-3) / 1e9
+    res["q8_0_gemv"] = {"workload": f"Q8_0 GEMV M=1 K={k} N={n}, bf16 activations, f32 out",
+                        "kernel_us": round(t * 1e3, 3), "weight_bytes": wbytes,
+                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    del ms
+    log("q8_0 gemv:", res["q8_0_gemv"])
+    # layer GEMMs at M = 256
+    layers = [("q", jq.Q4K, 4096, 3840), ("k", jq.Q4K, 2048, 3840), ("v", jq.Q4K, 2048, 3840),
+              ("o", jq.Q4K, 3840, 4096), ("gate_up", jq.Q4K, 30720, 3840), ("down", jq.Q6K, 3840, 15360)]
+    m = 256
+    per, tsum, fsum = {}, 0.0, 0.0
+    for name, kind, n, k in layers:
+        ms, _ = mats(kind, n, k, 2, 5)
+        x = xrows(m, k, 2)
+        out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        plan = jq.Plan.auto(ms[0], m, row_invariant=True)
+        jq.matmul_plan(gpu, x, m, ms[0], out, scratch, plan)
+        t = kernel_time_ms(lambda r: jq.matmul_plan(gpu, x, m, ms[r % 2], out, scratch, plan),
+                           max(4, steps // 4))
+        flops = 2.0 * m * n * k
+        per[name] = {"n": n, "k": k, "format": "Q6_K" if kind == jq.Q6K else "Q4_K",
+                     "plan": [plan.bm, plan.bn, plan.splits], "us": round(t * 1e3, 2),
+                     "tflops": round(flops / (t * 1e-3) / 1e12, 1)}
+        tsum += t
+        fsum += flops
+        del ms
+    tf = fsum / (tsum * 1e-3) / 1e12
+    res["layer_gemms_m256"] = {"workload": "one transformer block's six GEMMs at M=256, bf16 activations, f32 out",
+                               "gemms": per, "total_us": round(tsum * 1e3, 2),
+                               "roofline": {"bound": "mfma", "achieved": round(tf, 1),
+                                            "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                            "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}}
+    log("layer gemms:", res["layer_gemms_m256"])
+    # Q6_K vocabulary projection and argmax
+    n, k = 262144, 3840
+    ms, wbytes = mats(jq.Q6K, n, k, 1, 4)
+    lm = {}
+    for m in (1, 8, 32):
+        x = xrows(m, k, 3)
+        out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        jq.matmul(gpu, x, m, ms[0], out, scratch)
+        jq.argmax_rows(gpu, out, scratch)
+        t = kernel_time_ms(lambda r: jq.matmul(gpu, x, m, ms[0], out, scratch), max(4, steps // 10))
+        ta = kernel_time_ms(lambda r: jq.argmax_rows(gpu, out, scratch), max(4, steps // 10))
+        gbs = wbytes / (t * 1e-3) / 1e9
+        lm[str(m)] = {"kernel_us": round(t * 1e3, 2), "weight_GBps": round(gbs, 1),
+                      "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                      "tflops": round(2.0 * m * n * k / (t * 1e-3) / 1e12, 1),
+                      "argmax_us": round(ta * 1e3, 2)}
+    del ms
+    res["q6k_lm_head"] = {"workload": f"Q6_K vocabulary projection K={k} N={n} + per-row argmax, bf16 activations, f32 logits",
+                          "weight_bytes": wbytes, "per_m": lm}
+    log("q6k lm_head:", res["q6k_lm_head"])
+    return res
+
+
 def cpu_baseline(raw, n, k, x32):
     import oracle as O
 
@@ -233,6 +322,7 @@ def main():
     ap.add_argument("--gemm-steps", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the Q8_0, layer and lm_head lines")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.pmc_child:
@@ -328,6 +418,8 @@ def main():
     }
     log("gemm:", gemm)
 
+    configs = None if args.no_configs else measure_configs(gpu, 100)
+
     cpu = None if args.no_cpu else cpu_baseline(raw, n, k, x8)
     if cpu:
         log("cpu:", cpu)
@@ -373,6 +465,7 @@ def main():
         },
         "traffic_detail": traffic_detail,
         "gemm": gemm,
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
