@@ -405,9 +405,13 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
             return launch(ctx, name, dim3((unsigned)((T + tw - 1) / tw)), dim3(64 * waves), lds, stream, args);
         }
     }
-    if (plan.bm == 256) {
-        // Activations -> packed FP16 fragments, then the 256 x 128 Q4_K product.
-        const int mtiles = (int)((m + 255) / 256) * 16;
+    // Pipelined tile kernels (256 x 128, 128 x 128, 64 x 64; whole K in 256-element blocks):
+    // activations -> packed FP16 fragments, then the product. Every output element is the same
+    // MFMA chain as in the generic tile kernel, so the plans give the same bits.
+    if (plan.splits == 1 && w->k % 256 == 0 &&
+        ((plan.bm == 256 && plan.bn == 128) || (plan.bm == 128 && plan.bn == 128) ||
+         (plan.bm == 64 && plan.bn == 64))) {
+        const int mtiles = (int)((m + plan.bm - 1) / plan.bm) * (int)(plan.bm / 16);
         const size_t need = (size_t)mtiles * 16 * w->k * 2;
         if (ctx->pack_bytes < need) {
             if (ctx->pack) JV_HIP(hipFree(ctx->pack));
@@ -431,15 +435,20 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         GemmParams gp{};
         gp.xa = (const uint16_t *)ctx->pack;
         gp.wq = w->q;
+        gp.wh = w->h;
+        gp.wd = w->d;
         gp.out = out;
         gp.M = (int32_t)m;
-        gp.N = (int32_t)w->n;
+        gp.N = (int32_t)(w->n * w->experts);
         gp.K = (int32_t)w->k;
-        gp.ldo = (int32_t)w->n;
+        gp.ldo = (int32_t)(w->n * w->experts);
         gp.out_type = (int32_t)out_type;
         void *gargs[] = {&gp};
-        return launch(ctx, "jv_gemm_q4k_256x128", dim3((unsigned)(w->n / 128), (unsigned)(mtiles / 16)),
-                      dim3(512), 4 * 24 * 1024, stream, gargs);
+        char name[40];
+        snprintf(name, sizeof name, "jv_gemm_%s_%ux%u", fmt_kernel_name(w->fmt), plan.bm, plan.bn);
+        const unsigned waves = plan.bm >= 128 ? 8 : 4;
+        return launch(ctx, name, dim3((unsigned)(w->n * w->experts / plan.bn), (unsigned)(mtiles * 16 / plan.bm)),
+                      dim3(64 * waves), 4 * (plan.bm + plan.bn) / 16 * 1024, stream, gargs);
     }
     const int MT = plan_mt(plan), NT = plan_nt(plan);
     const int KU = fmt_unit(w->fmt);
@@ -749,10 +758,15 @@ jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
     if (!w) return jv_plan{0, 0, 0};
     if (m <= 16) return jv_plan{0, 64, 1};
     const size_t cus = w->ctx ? (size_t)std::max(1, w->ctx->info.compute_units) : 256;
-    // Q4_K with enough rows for one 256 x 128 workgroup per compute unit (or nearly)
-    if (w->fmt == JV_FMT_Q4K && w->n % 128 == 0 && m >= 256 &&
-        ((m + 255) / 256) * (w->n / 128) * 16 >= cus * 15)
-        return jv_plan{256, 128, 1};
+    const size_t cols = w->n * w->experts;
+    // Pipelined tiles (whole K, so row invariant): 256 x 128 when that gives about one workgroup
+    // per compute unit (each weight decoded once per 256 rows); otherwise 64 x 64, which keeps
+    // more compute units busy on narrow matrices. Fewer rows take the generic tiles.
+    if (w->k % 256 == 0 && m >= 48) {
+        if (cols % 128 == 0 && m >= 128 && ((m + 255) / 256) * (cols / 128) * 16 >= cus * 15)
+            return jv_plan{256, 128, 1};
+        if (cols % 64 == 0) return jv_plan{64, 64, 1};
+    }
     const uint32_t bm = m <= 32 ? 32 : (m <= 64 ? 64 : 128);
     const size_t mtiles = (m + bm - 1) / bm;
     uint32_t bn = 64;
@@ -775,9 +789,8 @@ jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
 int jv_plan_valid(const jv_qmatrix *w, size_t m, jv_plan p) {
     if (!w) return 0;
     if (p.bm == 0) return m <= 16 && p.splits == 1;
-    // gfx950 Q4_K tile: 256 rows x 128 columns, whole K (no split)
-    if (p.bm == 256)
-        return w->fmt == JV_FMT_Q4K && p.bn == 128 && p.splits == 1 && w->n % 128 == 0;
+    // gfx950 tile: 256 rows x 128 columns, whole K (no split)
+    if (p.bm == 256) return p.bn == 128 && p.splits == 1 && w->n % 128 == 0 && w->k % 256 == 0;
     const bool bm_ok = p.bm == 32 || p.bm == 64 || p.bm == 128;
     const bool bn_ok = p.bn == 64 || p.bn == 128 || p.bn == 256;
     return bm_ok && bn_ok && w->n % p.bn == 0 && p.splits >= 1 && p.splits <= 16 &&

@@ -1302,21 +1302,66 @@ __device__ __forceinline__ f16x8 q4k_sub_frag(const Q4KItem &it, int j, float ds
 
 // WM x WN waves; wave w = WN mq + nh computes m-tiles MT mq .. +MT and n-tiles NT nh .. +NT
 // (MT = 16 / WM, NT = 8 / WN) of the 256 x 128 tile.
-template <int WM, int WN>
-__device__ __forceinline__ void gemm_q4k_body(const GemmParams &p) {
-    constexpr int W = WM * WN, MT = 16 / WM, NT = 8 / WN;
+// Weight-fragment decoders of the tiled product. SPU = 32-k stages per K unit; load() reads the
+// lane's raw bytes of weight row 16 tile + r for unit u, prep() its scales, frag() the FP16
+// B fragment of stage s of the unit (lane (g, r): row r, k = 32 s + 8 g .. +8).
+struct DQ4K {  // Q4_K: head dwords gathered across lane groups (q4k_row_scales)
+    static constexpr int SPU = 8;
+    typedef Q4KItem Raw;
+    struct Prep {
+        float dsc[8], dmm[8];
+    };
+    __device__ static void load(Raw &it, const GemmParams &p, int tile, int u, int g, int r) {
+        q4k_item_load(it, p.wq, p.K, tile, u, g, r);
+    }
+    __device__ static void prep(const Raw &it, Prep &pp, int g) { q4k_row_scales(it.hv, g, pp.dsc, pp.dmm); }
+    __device__ static f16x8 frag(const Raw &it, const Prep &pp, int s, int) {
+        return q4k_sub_frag(it, s, pp.dsc[s], pp.dmm[s]);
+    }
+};
+template <class F>
+struct DF {  // any format with the F* interface of the small-tile kernel
+    static constexpr int SPU = F::KU / 32;
+    typedef typename F::Raw Raw;
+    typedef typename F::Prep Prep;
+    __device__ static void load(Raw &raw, const GemmParams &p, int tile, int u, int g, int r) {
+        F::load(raw, p.wq, p.wh, p.wd, p.K, tile * 16 + r, u, g);
+    }
+    __device__ static void prep(const Raw &raw, Prep &pp, int g) { F::prep(raw, pp, g); }
+    __device__ static f16x8 frag(const Raw &raw, const Prep &pp, int s, int g) { return frag_f16<F>(raw, pp, s, g); }
+};
+
+// Tiled product over packed activation fragments: a workgroup of WM x WN waves computes a
+// (16 TM) x (16 TN) output tile; wave w = WN mq + nh computes m-tiles MT mq .. +MT and n-tiles
+// NT nh .. +NT (MT = TM / WM, NT = TN / WN), MT x NT MFMA 16x16x32 accumulators. K advances
+// in 32-k stages through four LDS buffers of (TM + TN) KB: per stage, wave w copies AS = TM / W
+// activation fragments (1 KB each, lane order) from jv_pack_x's output and decodes BS = TN / W
+// weight fragments (D::frag, the reference's FP16 tile format), so every weight is decoded once
+// per workgroup. A wave takes the fragments it wrote from its registers and reads the others
+// from LDS; the reads for stage t + 1 are issued while stage t's MFMAs run, and stage t + 2 is
+// written meanwhile. Raw weights are loaded 8 stages ahead. Register slots are ordered
+// own-first, so which fragment is whose is fixed at compile time. Requires K % 256 == 0.
+//
+// Each output element is the same MFMA chain over K as in the other tiled kernels (32-k steps
+// in order, lane group g holding k 32s + 8g .. +8), so the result is bitwise identical to theirs.
+template <class D, int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void gemm_body(const GemmParams &p) {
+    constexpr int W = WM * WN, MT = TM / WM, NT = TN / WN;
     constexpr int AS = MT / WN;  // activation fragments a wave stages per stage (own m slots)
     constexpr int BS = NT / WM;  // weight fragments a wave decodes per stage (own n slots)
-    static_assert(AS * W == 16 && BS * W == 8, "tile split");
+    constexpr int UPS = 8 / D::SPU;  // K units per 8 stages
+    constexpr int BUF = (TM + TN) * 1024;
+    static_assert(AS * W == TM && BS * W == TN && AS >= 1 && BS >= 1, "tile split");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, r = lane & 15;
     const int mq = w / WN, nh = w % WN;
-    const int U = p.K >> 8;
-    const int mt0 = blockIdx.y * 16;  // first 16-row activation tile
-    const int t0 = blockIdx.x * 8;    // first 16-row weight tile
-    const int stages = 8 * U;
+    const int U8 = p.K >> 8;          // blocks of 8 stages
+    const int UK = U8 * UPS;          // K units
+    const int mt0 = blockIdx.y * TM;  // first 16-row activation tile
+    const int t0 = blockIdx.x * TN;   // first 16-row weight tile
+    const int stages = 8 * U8;
     const uint32_t lo16 = (uint32_t)lane * 16u;  // this lane's bytes in a 1 KB fragment
 
     // Local m-tile of slot i: own slots first (the AS this wave stages), then the rest of the
@@ -1330,36 +1375,41 @@ __device__ __forceinline__ void gemm_q4k_body(const GemmParams &p) {
         return NT * nh + (k < BS ? own0 + k : ((own0 + k) % NT));
     };
 
-    // The packed fragment of m-tile mt at stage st is fragment (mt U) 8 + st: consecutive
+    // The packed fragment of m-tile mt at stage st is fragment mt (K / 32) + st: consecutive
     // stages of one m-tile are consecutive 1 KB fragments.
     const uint8_t *xa_own[AS];
 #pragma unroll
     for (int i = 0; i < AS; ++i)
-        xa_own[i] = (const uint8_t *)p.xa + (size_t)(mt0 + m_of(i)) * (size_t)U * 8192u + lo16;
+        xa_own[i] = (const uint8_t *)p.xa + (size_t)(mt0 + m_of(i)) * (size_t)stages * 1024u + lo16;
     auto load_a = [&](u32x4 *dst, int st) __attribute__((always_inline)) {
         const uint32_t off = (uint32_t)min(st, stages - 1) * 1024u;
 #pragma unroll
         for (int i = 0; i < AS; ++i) dst[i] = *(const u32x4 *)(xa_own[i] + off);
     };
     // four LDS buffers, stage st in buffer st % 4 (a compile-time index in the unrolled loop)
-    auto buf_of = [&](int st) __attribute__((always_inline)) { return smem + (st & 3) * kGemmBufBytes + lo16; };
+    auto buf_of = [&](int st) __attribute__((always_inline)) { return smem + (st & 3) * BUF + lo16; };
     auto store_a = [&](const u32x4 *src, int st) __attribute__((always_inline)) {
         uint8_t *base = buf_of(st);
 #pragma unroll
         for (int i = 0; i < AS; ++i) *(u32x4 *)(base + m_of(i) * 1024) = src[i];
     };
-    auto load_w = [&](Q4KItem *dst, int u) __attribute__((always_inline)) {
+    // raw weights of the 8 stages from stage 8 b on (K units UPS b .. UPS b + UPS - 1)
+    auto load_w = [&](typename D::Raw (*dst)[BS], int b) __attribute__((always_inline)) {
 #pragma unroll
-        for (int k = 0; k < BS; ++k) q4k_item_load(dst[k], p.wq, p.K, t0 + n_of(k), min(u, U - 1), g, r);
+        for (int q = 0; q < UPS; ++q)
+#pragma unroll
+            for (int k = 0; k < BS; ++k) D::load(dst[q][k], p, t0 + n_of(k), min(UPS * b + q, UK - 1), g, r);
     };
-    float dsc[BS][8], dmm[BS][8];
-    auto block_scales = [&](const Q4KItem *it) __attribute__((always_inline)) {
+    typename D::Prep pp[UPS][BS];
+    auto block_prep = [&](const typename D::Raw (*it)[BS]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int k = 0; k < BS; ++k) q4k_row_scales(it[k].hv, g, dsc[k], dmm[k]);
+        for (int q = 0; q < UPS; ++q)
+#pragma unroll
+            for (int k = 0; k < BS; ++k) D::prep(it[q][k], pp[q][k], g);
     };
     auto store_b = [&](const f16x8 *v, int st) __attribute__((always_inline)) {
 #pragma unroll
-        for (int k = 0; k < BS; ++k) *(f16x8 *)(buf_of(st) + 16 * 1024 + n_of(k) * 1024) = v[k];
+        for (int k = 0; k < BS; ++k) *(f16x8 *)(buf_of(st) + TM * 1024 + n_of(k) * 1024) = v[k];
     };
     // the fragments of stage st this wave does not hold
     auto read_other = [&](f16x8 *fa, f16x8 *fb, int st) __attribute__((always_inline)) {
@@ -1367,7 +1417,7 @@ __device__ __forceinline__ void gemm_q4k_body(const GemmParams &p) {
 #pragma unroll
         for (int i = 0; i < MT - AS; ++i) fa[i] = *(const f16x8 *)(base + m_of(AS + i) * 1024);
 #pragma unroll
-        for (int k = 0; k < NT - BS; ++k) fb[k] = *(const f16x8 *)(base + 16 * 1024 + n_of(BS + k) * 1024);
+        for (int k = 0; k < NT - BS; ++k) fb[k] = *(const f16x8 *)(base + TM * 1024 + n_of(BS + k) * 1024);
     };
 
     f32x4 acc[MT][NT];
@@ -1386,23 +1436,26 @@ __device__ __forceinline__ void gemm_q4k_body(const GemmParams &p) {
                 acc[i][k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, k < BS ? bown[k] : fb[k - BS], acc[i][k], 0, 0, 0);
         }
     };
+    auto decode = [&](f16x8 *dst, const typename D::Raw (*it)[BS], int j) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < BS; ++k) dst[k] = D::frag(it[j / D::SPU][k], pp[j / D::SPU][k], j % D::SPU, g);
+    };
 
     // Register sets: own activation fragments of stages t .. t + 3 (index t % 4), own decoded
     // weight fragments of stages t .. t + 2 (index t % 4), other fragments read from LDS for
     // stages t, t + 1 (index t % 2).
-    Q4KItem cur[BS], nxt[BS];
+    typename D::Raw cur[UPS][BS], nxt[UPS][BS];
     u32x4 A[4][AS];
     f16x8 B[4][BS];
-    f16x8 FA[2][MT - AS], FB[2][NT - BS];
+    f16x8 FA[2][MT - AS > 0 ? MT - AS : 1], FB[2][NT - BS > 0 ? NT - BS : 1];
     load_w(cur, 0);
     load_w(nxt, 1);
 #pragma unroll
     for (int t = 0; t < 4; ++t) load_a(A[t], t);
-    block_scales(cur);
+    block_prep(cur);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int k = 0; k < BS; ++k) B[t][k] = q4k_sub_frag(cur[k], t, dsc[k][t], dmm[k][t]);
+        decode(B[t], cur, t);
         store_b(B[t], t);
         store_a(A[t], t);
     }
@@ -1419,14 +1472,15 @@ __device__ __forceinline__ void gemm_q4k_body(const GemmParams &p) {
         const int j2 = (j + 2) & 7;
         if (!tail || st + 1 < stages) read_other(FA[f ^ 1], FB[f ^ 1], st + 1);
         if (!tail || st + 2 < stages) {
-            if (j2 == 0) {  // stage st + 2 starts a block: its raw weights are in nxt
+            if (j2 == 0) {  // stage st + 2 starts a block of 8: its raw weights are in nxt
 #pragma unroll
-                for (int k = 0; k < BS; ++k) cur[k] = nxt[k];
+                for (int q = 0; q < UPS; ++q)
+#pragma unroll
+                    for (int k = 0; k < BS; ++k) cur[q][k] = nxt[q][k];
                 load_w(nxt, (st + 2) / 8 + 1);
-                block_scales(cur);
+                block_prep(cur);
             }
-#pragma unroll
-            for (int k = 0; k < BS; ++k) B[(c + 2) & 3][k] = q4k_sub_frag(cur[k], j2, dsc[k][j2], dmm[k][j2]);
+            decode(B[(c + 2) & 3], cur, j2);
             store_b(B[(c + 2) & 3], st + 2);
             store_a(A[(c + 2) & 3], st + 2);
         }
@@ -1448,12 +1502,12 @@ __device__ __forceinline__ void gemm_q4k_body(const GemmParams &p) {
         }
         lds_barrier();
     };
-    for (int b = 0; b + 1 < U; ++b) {
+    for (int b = 0; b + 1 < U8; ++b) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) step(8 * b + j, j, false);
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) step(8 * (U - 1) + j, j, true);
+    for (int j = 0; j < 8; ++j) step(8 * (U8 - 1) + j, j, true);
 
     // epilogue: lane (g, r) holds column r, rows 4g .. 4g + 3 of each 16 x 16 tile
     const bool f32_out = p.out_type == 0;
@@ -1477,7 +1531,19 @@ __device__ __forceinline__ void gemm_q4k_body(const GemmParams &p) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(512) void jv_gemm_q4k_256x128(GemmParams p) { gemm_q4k_body<4, 2>(p); }
+// Tiles (rows x columns): 256 x 128 and 128 x 128 on 8 waves, 64 x 64 on 4.
+#define JV_GEMM(NAME, D, TM, TN, WM, WN, ROWS, COLS)                                          \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN) void jv_gemm_##NAME##_##ROWS##x##COLS(GemmParams p) { \
+        gemm_body<D, TM, TN, WM, WN>(p);                                                      \
+    }
+#define JV_GEMM_TILES(NAME, D)                                                                \
+    JV_GEMM(NAME, D, 16, 8, 4, 2, 256, 128) JV_GEMM(NAME, D, 8, 8, 4, 2, 128, 128)          \
+    JV_GEMM(NAME, D, 4, 4, 2, 2, 64, 64)
+JV_GEMM_TILES(q4k, DQ4K)
+JV_GEMM_TILES(q6k, DF<FQ6K>)
+JV_GEMM_TILES(q8_0, DF<FQ8_0>)
+JV_GEMM_TILES(q5_0, DF<FQ5_0>)
+JV_GEMM_TILES(f16, DF<FF16>)
 
 // ---------------------------------------------------------------------------------------------
 // Repack GGML blocks (device copy) into the device layouts above.

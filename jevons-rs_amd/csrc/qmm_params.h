@@ -41,10 +41,12 @@ struct PackXParams {
     int32_t mtiles;      // 16-row tiles packed (M rounded up to the product's row tile)
 };
 
-// Q4_K 256 x 128-tile product over packed activation fragments (jv_pack_x output).
+// Tiled product over packed activation fragments (jv_pack_x output).
 struct GemmParams {
     const uint16_t *xa;  // packed activations
-    const uint8_t *wq;   // Q4_K tile layout
+    const uint8_t *wq;   // weight regions of the format's device layout
+    const uint8_t *wh;
+    const uint8_t *wd;
     void *out;           // [M][ldo] of `out_type`
     int32_t M, N, K, ldo, out_type;
 };

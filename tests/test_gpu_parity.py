@@ -408,8 +408,10 @@ def test_plan_rules_follow_the_reference(gpu):
     assert not jq.Plan(0, 128, 2).valid_for(w, 4)
     assert jq.Plan(128, 128, 8).valid_for(w, 4) and not jq.Plan(128, 128, 9).valid_for(w, 4)
     assert not jq.Plan(128, 128, 0).valid_for(w, 4)
-    # the gfx950 256 x 128 tile exists for Q4_K only, without split-K
-    assert not jq.Plan(256, 128, 1).valid_for(w, 512)
+    # the gfx950 256 x 128 tile: any format, whole K in 256-element blocks, no split-K
+    assert jq.Plan(256, 128, 1).valid_for(w, 512)
+    w320 = jq.QMatrix.upload(gpu, jq.Q8_0, 256, 320, 1, synth.weights(jq.Q8_0, 1, 256, 320))
+    assert not jq.Plan(256, 128, 1).valid_for(w320, 512)
     w4 = jq.QMatrix.upload(gpu, jq.Q4K, 256, 512, 1, synth.weights(jq.Q4K, 1, 256, 512))
     assert jq.Plan(256, 128, 1).valid_for(w4, 512)
     assert not jq.Plan(256, 128, 2).valid_for(w4, 512) and not jq.Plan(256, 64, 1).valid_for(w4, 512)
