@@ -145,6 +145,41 @@ jv_status jv_matmul_split(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, 
                           uint32_t bm, uint32_t bn, uint32_t splits, jv_scratch *scratch,
                           void *stream);
 
+/* Expert grouping produced on the device (Groups, gemm.rs:955-966): sorted assignment ids,
+ * per-expert offsets [experts + 1] and jobs (jobs[0] = count, then (expert, start) pairs), all
+ * device uint32 buffers; max_jobs bounds the job count (the grid); input row = id / in_div;
+ * rows = output rows (assignments). */
+typedef struct {
+    const uint32_t *ids;
+    const uint32_t *offsets;
+    const uint32_t *jobs;
+    size_t max_jobs;
+    uint32_t in_div;
+    size_t rows;
+} jv_groups;
+
+/* Expert grouping of routed assignments (ops::group_routes / group,
+ * crates/jevons-gemma4-diffusion/src/gpu/ops.rs:1100-1130 and :522-587): device ids
+ * [assignments] -> sorted [assignments], offsets [experts + 1], jobs [jobs_len] for row tiles
+ * of bm. Ids >= experts are not routed. experts <= 1024; jobs_len must hold
+ * 1 + 2 * (ceil(assignments / bm) + experts) words. */
+jv_status jv_group_routes(jv_ctx *ctx, const uint32_t *ids, size_t assignments, size_t experts,
+                          uint32_t bm, uint32_t *sorted, uint32_t *offsets, uint32_t *jobs,
+                          size_t jobs_len, void *stream);
+/* Expert-grouped product (matmul_grouped, gemm.rs:1274-1321): job j multiplies up to bm sorted
+ * rows of expert e by that expert's weight rows [e n, (e + 1) n) and writes output rows ids[s]
+ * of out [g.rows, n]. bm in {16, 32, 64, 128}, bn in {64, 128, 256}; splits > 1 divides K and
+ * sums the partials in `scratch`. */
+jv_status jv_matmul_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len,
+                            const jv_qmatrix *w, const jv_groups *g, void *out, jv_out out_type,
+                            size_t out_len, uint32_t bm, uint32_t bn, uint32_t splits,
+                            jv_scratch *scratch, void *stream);
+/* Expert-grouped small-row product (matvec_grouped, gemm.rs:1171-1203): jobs of at most
+ * mr <= 16 rows. */
+jv_status jv_matvec_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len,
+                            const jv_qmatrix *w, const jv_groups *g, void *out, jv_out out_type,
+                            size_t out_len, uint32_t mr, void *stream);
+
 /* Burn operator GemmOps::f16_matmul (crates/jevons-burn/src/kernels.rs:52-97): dense row-major
  * FP16 x [m, k] times FP16 weight [n, k]^T into FP32 out [m, n], with the row-invariant plan
  * rule of kernels.rs:16-31. n and k must be multiples of 64. */

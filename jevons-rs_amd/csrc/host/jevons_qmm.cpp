@@ -329,6 +329,88 @@ int plan_nt(const jv_plan &p) { return p.bm == 0 ? 1 : (int)p.bn / 64; }
 bool act_ok(jv_act a) { return a == JV_ACT_F16 || a == JV_ACT_BF16 || a == JV_ACT_F32; }
 bool out_ok(jv_out o) { return o == JV_OUT_F32 || o == JV_OUT_BF16; }
 
+// Expert-grouped launch arguments (Groups, gemm.rs:955-966) plus the rows per job.
+struct GroupArgs {
+    const uint32_t *ids, *offsets, *jobs;
+    size_t max_jobs;
+    uint32_t in_div;
+    uint32_t cap;
+};
+
+// The generic tile kernel (any plan, split-K through the scratch buffer and jv_reduce_splits).
+// m = output rows; grouped launches cover grp->max_jobs jobs of at most grp->cap rows.
+jv_status launch_tiles(jv_ctx *ctx, const void *x, jv_act act, size_t m, const jv_qmatrix *w,
+                       void *out, jv_out out_type, jv_scratch *scratch, jv_plan plan, void *stream,
+                       const GroupArgs *grp) {
+    jv_status st = JV_OK;
+    const int MT = plan_mt(plan), NT = plan_nt(plan);
+    const int KU = fmt_unit(w->fmt);
+    const int splits = (int)plan.splits;
+    const int U = (int)(w->k / KU);
+    const int max_units = (U + splits - 1) / splits;
+    const int rows_alloc = (int)std::min<size_t>((size_t)(16 * MT), grp ? (size_t)grp->cap : m);
+    // LDS budget for the staged activation chunk: whole K for small tiles when it fits.
+    const size_t budget = MT == 1 ? 128 * 1024 : 80 * 1024;
+    int kc_units = (int)((budget / (2 * (size_t)rows_alloc) - 8) / (size_t)KU);
+    kc_units = std::max(1, std::min(kc_units, max_units));
+    const int kc = kc_units * KU;
+    const size_t lds = (size_t)rows_alloc * (size_t)(kc + 8) * 2;
+    if (lds > ctx->info.lds_bytes)
+        return fail(JV_ERR_INVALID, "tile needs %zu bytes of LDS, the device has %zu", lds,
+                    ctx->info.lds_bytes);
+
+    QmmParams p{};
+    p.x = x;
+    p.wq = w->q;
+    p.wh = w->h;
+    p.wd = w->d;
+    p.M = (int32_t)m;
+    p.N = (int32_t)w->n;
+    p.K = (int32_t)w->k;
+    p.ldx = (int32_t)w->k;
+    p.ldo = (int32_t)w->n;
+    p.act = (int32_t)act;
+    p.out_type = (int32_t)out_type;
+    p.kc = kc;
+    p.splits = splits;
+    p.split_stride = (int64_t)(m * w->n);
+    if (grp) {
+        p.grouped = 1;
+        p.ids = grp->ids;
+        p.offsets = grp->offsets;
+        p.jobs = grp->jobs;
+        p.in_div = (int32_t)grp->in_div;
+        p.rows_cap = (int32_t)grp->cap;
+    }
+    if (splits > 1) {
+        if (!scratch) return fail(JV_ERR_INVALID, "split-K plans need a scratch buffer");
+        const size_t need = (size_t)splits * m * w->n * 4;
+        if (scratch->bytes < need) {
+            if (scratch->buf) JV_HIP(hipFree(scratch->buf));
+            scratch->buf = nullptr;
+            scratch->bytes = 0;
+            JV_HIP(hipMalloc(&scratch->buf, need));
+            scratch->bytes = need;
+        }
+        p.out = scratch->buf;
+    } else {
+        p.out = out;
+    }
+    char name[64];
+    snprintf(name, sizeof name, "jv_qmm_%s_m%d_n%d", fmt_kernel_name(w->fmt), MT, NT);
+    const size_t gy = grp ? grp->max_jobs : (m + 16 * MT - 1) / (16 * MT);
+    dim3 grid((unsigned)(w->n / (size_t)(64 * NT)), (unsigned)gy, (unsigned)splits);
+    void *args[] = {&p};
+    st = launch(ctx, name, grid, dim3(256), lds, stream, args);
+    if (st != JV_OK || splits == 1) return st;
+    const void *part = scratch->buf;
+    int64_t len = (int64_t)(m * w->n);
+    int sp = splits, ot = (int)out_type;
+    void *rargs[] = {&part, &out, &len, &sp, &ot};
+    return launch(ctx, "jv_reduce_splits", dim3((unsigned)((len + 255) / 256)), dim3(256), 0,
+                  stream, rargs);
+}
+
 jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
                       const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
                       jv_plan plan, jv_scratch *scratch, void *stream) {
@@ -450,64 +532,7 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         return launch(ctx, name, dim3((unsigned)(w->n * w->experts / plan.bn), (unsigned)(mtiles * 16 / plan.bm)),
                       dim3(64 * waves), 4 * (plan.bm + plan.bn) / 16 * 1024, stream, gargs);
     }
-    const int MT = plan_mt(plan), NT = plan_nt(plan);
-    const int KU = fmt_unit(w->fmt);
-    const int splits = (int)plan.splits;
-    const int U = (int)(w->k / KU);
-    const int max_units = (U + splits - 1) / splits;
-    const int rows_alloc = (int)std::min<size_t>((size_t)(16 * MT), m);
-    // LDS budget for the staged activation chunk: whole K for small tiles when it fits.
-    const size_t budget = MT == 1 ? 128 * 1024 : 80 * 1024;
-    int kc_units = (int)((budget / (2 * (size_t)rows_alloc) - 8) / (size_t)KU);
-    kc_units = std::max(1, std::min(kc_units, max_units));
-    const int kc = kc_units * KU;
-    const size_t lds = (size_t)rows_alloc * (size_t)(kc + 8) * 2;
-    if (lds > ctx->info.lds_bytes)
-        return fail(JV_ERR_INVALID, "tile needs %zu bytes of LDS, the device has %zu", lds,
-                    ctx->info.lds_bytes);
-
-    QmmParams p{};
-    p.x = x;
-    p.wq = w->q;
-    p.wh = w->h;
-    p.wd = w->d;
-    p.M = (int32_t)m;
-    p.N = (int32_t)w->n;
-    p.K = (int32_t)w->k;
-    p.ldx = (int32_t)w->k;
-    p.ldo = (int32_t)w->n;
-    p.act = (int32_t)act;
-    p.out_type = (int32_t)out_type;
-    p.kc = kc;
-    p.splits = splits;
-    p.split_stride = (int64_t)(m * w->n);
-    if (splits > 1) {
-        if (!scratch) return fail(JV_ERR_INVALID, "split-K plans need a scratch buffer");
-        const size_t need = (size_t)splits * m * w->n * 4;
-        if (scratch->bytes < need) {
-            if (scratch->buf) JV_HIP(hipFree(scratch->buf));
-            scratch->buf = nullptr;
-            scratch->bytes = 0;
-            JV_HIP(hipMalloc(&scratch->buf, need));
-            scratch->bytes = need;
-        }
-        p.out = scratch->buf;
-    } else {
-        p.out = out;
-    }
-    char name[64];
-    snprintf(name, sizeof name, "jv_qmm_%s_m%d_n%d", fmt_kernel_name(w->fmt), MT, NT);
-    dim3 grid((unsigned)(w->n / (size_t)(64 * NT)), (unsigned)((m + 16 * MT - 1) / (16 * MT)),
-              (unsigned)splits);
-    void *args[] = {&p};
-    st = launch(ctx, name, grid, dim3(256), lds, stream, args);
-    if (st != JV_OK || splits == 1) return st;
-    const void *part = scratch->buf;
-    int64_t len = (int64_t)(m * w->n);
-    int sp = splits, ot = (int)out_type;
-    void *rargs[] = {&part, &out, &len, &sp, &ot};
-    return launch(ctx, "jv_reduce_splits", dim3((unsigned)((len + 255) / 256)), dim3(256), 0,
-                  stream, rargs);
+    return launch_tiles(ctx, x, act, m, w, out, out_type, scratch, plan, stream, nullptr);
 }
 
 jv_status dequant_rows(jv_ctx *ctx, const jv_qmatrix *w, size_t row0, size_t rows, void *out,
@@ -843,6 +868,78 @@ jv_status jv_matmul_split(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, 
     if (bm == 0) return fail(JV_ERR_INVALID, "matmul_split needs a row tile (bm > 0)");
     return run_product(ctx, x, act, x_len, m, w, out, out_type, out_len,
                        jv_plan{bm, bn, splits}, scratch, stream);
+}
+
+jv_status jv_group_routes(jv_ctx *ctx, const uint32_t *ids, size_t assignments, size_t experts,
+                          uint32_t bm, uint32_t *sorted, uint32_t *offsets, uint32_t *jobs,
+                          size_t jobs_len, void *stream) {
+    jv_status st = use_device(ctx);
+    if (st != JV_OK) return st;
+    if (experts == 0 || experts > 1024)
+        return fail(JV_ERR_INVALID, "grouping handles 1 to 1024 experts, got %zu", experts);
+    if (bm == 0) return fail(JV_ERR_INVALID, "row tile bm must be positive");
+    if (assignments > (size_t)UINT32_MAX) return fail(JV_ERR_INVALID, "too many routes");
+    if (jobs_len < 1 + 2 * ((assignments + bm - 1) / bm + experts))
+        return fail(JV_ERR_INVALID, "jobs buffer of %zu words is too small", jobs_len);
+    if ((assignments && (!ids || !sorted)) || !offsets || !jobs)
+        return fail(JV_ERR_INVALID, "null buffer");
+    uint32_t a = (uint32_t)assignments, e = (uint32_t)experts, b = bm;
+    void *args[] = {&ids, &a, &e, &b, &sorted, &offsets, &jobs};
+    return launch(ctx, "jv_group_routes", dim3(1), dim3(256), 0, stream, args);
+}
+
+namespace {
+// Checks shared by the grouped products (gemm.rs:1172, :1285).
+jv_status check_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, const jv_qmatrix *w,
+                        const jv_groups *g, void *out, size_t out_len) {
+    jv_status st = use_device(ctx);
+    if (st != JV_OK) return st;
+    if (!w || !g) return fail(JV_ERR_INVALID, "null matrix or groups");
+    if (act != JV_ACT_F16 && act != JV_ACT_BF16 && act != JV_ACT_F32)
+        return fail(JV_ERR_INVALID, "unknown activation type");
+    if (out_len < g->rows * w->n)
+        return fail(JV_ERR_INVALID, "output holds %zu values, grouped product writes %zu", out_len,
+                    g->rows * w->n);
+    if (g->in_div == 0) return fail(JV_ERR_INVALID, "in_div must be positive");
+    if (x_len < (g->rows + g->in_div - 1) / g->in_div * w->k)
+        return fail(JV_ERR_INVALID, "activations hold %zu values, need %zu", x_len,
+                    (g->rows + g->in_div - 1) / g->in_div * w->k);
+    if (g->rows && (!x || !out || !g->ids || !g->offsets || !g->jobs))
+        return fail(JV_ERR_INVALID, "null buffer");
+    if (((uintptr_t)x & 15u) != 0) return fail(JV_ERR_INVALID, "activations must be 16-byte aligned");
+    if (g->max_jobs > 65535) return fail(JV_ERR_INVALID, "max_jobs %zu is too large", g->max_jobs);
+    return JV_OK;
+}
+}  // namespace
+
+jv_status jv_matmul_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len,
+                            const jv_qmatrix *w, const jv_groups *g, void *out, jv_out out_type,
+                            size_t out_len, uint32_t bm, uint32_t bn, uint32_t splits,
+                            jv_scratch *scratch, void *stream) {
+    jv_status st = check_grouped(ctx, x, act, x_len, w, g, out, out_len);
+    if (st != JV_OK) return st;
+    if (bm != 16 && bm != 32 && bm != 64 && bm != 128)
+        return fail(JV_ERR_INVALID, "grouped row tile %u is not 16, 32, 64 or 128", bm);
+    if ((bn != 64 && bn != 128 && bn != 256) || w->n % bn != 0)
+        return fail(JV_ERR_INVALID, "n = %zu is not a multiple of the column tile %u", w->n, bn);
+    if (splits < 1 || splits > 16 || w->k / 64 < splits)
+        return fail(JV_ERR_INVALID, "splits = %u is out of range", splits);
+    if (g->rows == 0 || g->max_jobs == 0) return JV_OK;
+    GroupArgs ga{g->ids, g->offsets, g->jobs, g->max_jobs, g->in_div, bm};
+    return launch_tiles(ctx, x, act, g->rows, w, out, out_type, scratch, jv_plan{bm, bn, splits},
+                        stream, &ga);
+}
+
+jv_status jv_matvec_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len,
+                            const jv_qmatrix *w, const jv_groups *g, void *out, jv_out out_type,
+                            size_t out_len, uint32_t mr, void *stream) {
+    jv_status st = check_grouped(ctx, x, act, x_len, w, g, out, out_len);
+    if (st != JV_OK) return st;
+    if (mr == 0 || mr > 16) return fail(JV_ERR_INVALID, "matvec_grouped handles 1 to 16 rows per job");
+    if (g->rows == 0 || g->max_jobs == 0) return JV_OK;
+    GroupArgs ga{g->ids, g->offsets, g->jobs, g->max_jobs, g->in_div, mr};
+    return launch_tiles(ctx, x, act, g->rows, w, out, out_type, nullptr, jv_plan{16, 64, 1}, stream,
+                        &ga);
 }
 
 // crates/jevons-burn/src/kernels.rs:52-97 with the row-invariant plan rule of :16-31.

@@ -318,7 +318,8 @@ __device__ __forceinline__ f16x8 frag_f16(const typename F::Raw &r, const typena
 }
 
 // ---------------------------------------------------------------------------------------------
-// Activation staging: rows [m0, m0 + rows) x k [k0, k0 + kl) -> LDS FP16, row stride `stride`.
+// Activation staging: rows [m0, m0 + rows) x k [k0, k0 + kl) -> LDS FP16, row stride `stride`
+// (grouped: sorted positions m0 .. m0 + rows, each reading input row ids[s] / in_div).
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ void stage_rows(const QmmParams &p, _Float16 *lds, int m0, int rows,
                                            int k0, int kl, int stride) {
@@ -327,7 +328,8 @@ __device__ __forceinline__ void stage_rows(const QmmParams &p, _Float16 *lds, in
     for (int i = threadIdx.x; i < total; i += kThreads) {
         const int r = i / per_row;
         const int c8 = i - r * per_row;
-        const size_t src = (size_t)(m0 + r) * (size_t)p.ldx + (size_t)(k0 + 8 * c8);
+        const int xr = p.grouped ? (int)(p.ids[m0 + r] / (uint32_t)p.in_div) : m0 + r;
+        const size_t src = (size_t)xr * (size_t)p.ldx + (size_t)(k0 + 8 * c8);
         f16x8 v;
         if (p.act == 0) {
             v = __builtin_bit_cast(f16x8, *(const uint4 *)((const uint16_t *)p.x + src));
@@ -360,9 +362,18 @@ __device__ __forceinline__ void qmm_body(const QmmParams &p) {
     const int g = lane >> 4;
     const int r16 = lane & 15;
     const int n_base = (int)blockIdx.x * (kWaves * 16 * NT) + wave * 16 * NT;
-    const int m0 = (int)blockIdx.y * 16 * MT;
+    int m0 = (int)blockIdx.y * 16 * MT;
+    int rows_real = min(16 * MT, p.M - m0);
+    int wrow0 = 0;  // first weight row (the expert's in grouped mode)
+    if (p.grouped) {
+        const int job = blockIdx.y;
+        if (job >= (int)p.jobs[0]) return;  // the whole workgroup, before any barrier
+        const int expert = (int)p.jobs[1 + 2 * job];
+        m0 = (int)p.jobs[2 + 2 * job];
+        rows_real = min(min((int)p.offsets[expert + 1] - m0, p.rows_cap), 16 * MT);
+        wrow0 = expert * p.N;
+    }
     const bool active = n_base < p.N;
-    const int rows_real = min(16 * MT, p.M - m0);
     const int stride = p.kc + kLdsPad;
 
     const int U = p.K / F::KU;
@@ -381,7 +392,7 @@ __device__ __forceinline__ void qmm_body(const QmmParams &p) {
     if (active && u_first < u_last) {
 #pragma unroll
         for (int t = 0; t < NT; ++t)
-            F::load(cur[t], p.wq, p.wh, p.wd, p.K, n_base + 16 * t + r16, u_first, g);
+            F::load(cur[t], p.wq, p.wh, p.wd, p.K, wrow0 + n_base + 16 * t + r16, u_first, g);
     }
 
     int chunk_u0 = u_first;
@@ -397,7 +408,7 @@ __device__ __forceinline__ void qmm_body(const QmmParams &p) {
             if (u + 1 < u_last) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t)
-                    F::load(nxt[t], p.wq, p.wh, p.wd, p.K, n_base + 16 * t + r16, u + 1, g);
+                    F::load(nxt[t], p.wq, p.wh, p.wd, p.K, wrow0 + n_base + 16 * t + r16, u + 1, g);
             }
             typename F::Prep pp[NT];
 #pragma unroll
@@ -429,8 +440,9 @@ __device__ __forceinline__ void qmm_body(const QmmParams &p) {
     for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = m0 + mt * 16 + 4 * g + i;
-            if (row >= p.M) continue;
+            const int lr = mt * 16 + 4 * g + i;
+            if (lr >= rows_real) continue;
+            const int row = p.grouped ? (int)p.ids[m0 + lr] : m0 + lr;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const int col = n_base + 16 * t + r16;
@@ -1635,6 +1647,48 @@ extern "C" __global__ __launch_bounds__(256) void jv_repack_q5_0(RepackParams p)
 // Row argmax with greedy's rule (crates/jevons-core/src/model.rs:207-219): the first maximum
 // wins; any non-finite value makes the row invalid (-1).
 // ---------------------------------------------------------------------------------------------
+// Expert grouping (ops::group, crates/jevons-gemma4-diffusion/src/gpu/ops.rs:522-587), one
+// workgroup: sorted[] lists the assignments of expert 0, then 1, ... (each in assignment order),
+// offsets[e] is expert e's first sorted position (offsets[experts] = routed count), jobs[0] the
+// number of bm-row tiles and jobs[1 + 2j], jobs[2 + 2j] tile j's (expert, first position).
+// Ids >= experts are not routed. Thread t handles experts t, t + 256, ...; experts <= 1024.
+extern "C" __global__ __launch_bounds__(256) void jv_group_routes(const uint32_t *ids, uint32_t assignments,
+                                                                  uint32_t experts, uint32_t bm,
+                                                                  uint32_t *sorted, uint32_t *offsets,
+                                                                  uint32_t *jobs) {
+    __shared__ uint32_t counts[1024], starts[1025], jstarts[1025];
+    for (uint32_t e = threadIdx.x; e < experts; e += 256) {
+        uint32_t c = 0;
+        for (uint32_t a = 0; a < assignments; ++a) c += ids[a] == e;
+        counts[e] = c;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t acc = 0, jacc = 0;
+        for (uint32_t e = 0; e < experts; ++e) {
+            starts[e] = acc;
+            jstarts[e] = jacc;
+            acc += counts[e];
+            jacc += (counts[e] + bm - 1) / bm;
+        }
+        starts[experts] = acc;
+        offsets[experts] = acc;
+        jobs[0] = jacc;
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < experts; e += 256) {
+        offsets[e] = starts[e];
+        uint32_t next = starts[e];
+        for (uint32_t a = 0; a < assignments; ++a)
+            if (ids[a] == e) sorted[next++] = a;
+        const uint32_t tiles = (counts[e] + bm - 1) / bm;
+        for (uint32_t t = 0; t < tiles; ++t) {
+            jobs[1 + 2 * (jstarts[e] + t)] = e;
+            jobs[2 + 2 * (jstarts[e] + t)] = starts[e] + t * bm;
+        }
+    }
+}
+
 __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
     // (v, i) replaces (bv, bi) if larger, or equal with a lower index.
     if (v > bv || (v == bv && i < bi)) {

@@ -19,6 +19,11 @@ struct QmmParams {
     int32_t kc;          // K staged in LDS per chunk (multiple of the format's K unit)
     int32_t splits;      // grid z; slice z covers units [z*U/splits, (z+1)*U/splits)
     int64_t split_stride;  // elements between partial planes
+    // Expert-grouped mode (grid y = job; gemm.rs:9-11): job j covers sorted positions
+    // [jobs[2j+2], min(+rows_cap, offsets[e+1])) of expert e = jobs[2j+1]; position s reads
+    // input row ids[s] / in_div and writes output row ids[s]; weight rows start at e * N.
+    const uint32_t *ids, *offsets, *jobs;
+    int32_t grouped, in_div, rows_cap;
 };
 
 // Decode probe: rows [row0, row0 + rows) of a weight matrix into [rows][K].

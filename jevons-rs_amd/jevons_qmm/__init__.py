@@ -38,6 +38,11 @@ class JvError(RuntimeError):
         self.message = message
 
 
+class jv_groups(C.Structure):
+    _fields_ = [("ids", C.c_void_p), ("offsets", C.c_void_p), ("jobs", C.c_void_p),
+                ("max_jobs", C.c_size_t), ("in_div", C.c_uint32), ("rows", C.c_size_t)]
+
+
 class jv_plan(C.Structure):
     _fields_ = [("bm", C.c_uint32), ("bn", C.c_uint32), ("splits", C.c_uint32)]
 
@@ -86,6 +91,9 @@ def lib() -> C.CDLL:
         "jv_argmax_rows": (I, [P, P, S, S, P, P, P]),
         "jv_dequant_rows_f32": (I, [P, P, S, S, P, P]),
         "jv_dequant_rows_f16": (I, [P, P, S, S, P, P]),
+        "jv_group_routes": (I, [P, P, S, S, U32, P, P, P, S, P]),
+        "jv_matmul_grouped": (I, [P, P, I, S, P, C.POINTER(jv_groups), P, I, S, U32, U32, U32, P, P]),
+        "jv_matvec_grouped": (I, [P, P, I, S, P, C.POINTER(jv_groups), P, I, S, U32, P]),
         "jv_last_error": (C.c_char_p, []),
     }
     for name, (res, args) in sigs.items():
@@ -337,6 +345,50 @@ def f16_linear_scaled(gpu: Gpu, x, weight):
     x = x.to(torch.float32)
     scale = (x.abs().amax(dim=1, keepdim=True) / F16_ROW_LIMIT).clamp_min(1.0)
     return f16_linear(gpu, x / scale, weight) * scale
+
+
+class Groups:
+    """Expert grouping produced on the device (Groups, gemm.rs:955-966): `ids` (sorted assignment
+    ids), `offsets` [experts + 1] and `jobs` are device uint32 tensors (int32 storage)."""
+
+    def __init__(self, ids, offsets, jobs, max_jobs: int, in_div: int, rows: int):
+        self.ids, self.offsets, self.jobs = ids, offsets, jobs
+        self.max_jobs, self.in_div, self.rows = max_jobs, in_div, rows
+
+    def c(self) -> jv_groups:
+        return jv_groups(_dev(self.ids), _dev(self.offsets), _dev(self.jobs), self.max_jobs,
+                         self.in_div, self.rows)
+
+
+def group_routes(gpu: Gpu, ids, experts: int, bm: int, in_div: int = 1, stream=None) -> Groups:
+    """ops::group_routes (crates/jevons-gemma4-diffusion/src/gpu/ops.rs:1100-1130): groups the
+    routed assignments `ids` (device int32 expert per assignment) by expert for row tiles of bm."""
+    import torch
+
+    a = ids.numel()
+    max_jobs = (a + bm - 1) // bm + experts
+    sorted_ = torch.zeros(max(a, 1), dtype=torch.int32, device=ids.device)
+    offsets = torch.zeros(experts + 1, dtype=torch.int32, device=ids.device)
+    jobs = torch.zeros(1 + 2 * max_jobs, dtype=torch.int32, device=ids.device)
+    _check(lib().jv_group_routes(gpu.handle, _dev(ids), a, experts, bm, _dev(sorted_), _dev(offsets),
+                                 _dev(jobs), jobs.numel(), _stream(stream)))
+    return Groups(sorted_, offsets, jobs, max_jobs, in_div, a)
+
+
+def matmul_grouped(gpu: Gpu, x, w: QMatrix, g: Groups, out, bm: int, bn: int, splits: int,
+                   scratch: SplitScratch | None, stream=None):
+    """Expert-grouped product (matmul_grouped, gemm.rs:1274-1321)."""
+    gc = g.c()
+    _check(lib().jv_matmul_grouped(gpu.handle, _dev(x), _act(x), x.numel(), w.handle, C.byref(gc),
+                                   _dev(out), _out(out), out.numel(), bm, bn, splits, _sh(scratch),
+                                   _stream(stream)))
+
+
+def matvec_grouped(gpu: Gpu, x, w: QMatrix, g: Groups, out, mr: int, stream=None):
+    """Expert-grouped small-row product (matvec_grouped, gemm.rs:1171-1203)."""
+    gc = g.c()
+    _check(lib().jv_matvec_grouped(gpu.handle, _dev(x), _act(x), x.numel(), w.handle, C.byref(gc),
+                                   _dev(out), _out(out), out.numel(), mr, _stream(stream)))
 
 
 def argmax_rows(gpu: Gpu, logits, scratch: SplitScratch, stream=None):

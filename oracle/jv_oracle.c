@@ -281,6 +281,34 @@ int jvo_greedy(const float *row, size_t n, int32_t *index, double *prob) {
     return 0;
 }
 
+/* ops::group (crates/jevons-gemma4-diffusion/src/gpu/ops.rs:522-587): assignments sorted by
+ * expert, stable within an expert (sorted[...] = assignment index); offsets[e] = first sorted
+ * position of expert e, offsets[experts] = assignments; jobs[0] = job count, then one
+ * (expert, start) pair per bm-row tile of each expert, experts in order. Ids >= experts match no
+ * expert and are not routed, as in the reference kernel. Returns the job count. */
+int jvo_group_routes(const uint32_t *ids, size_t assignments, size_t experts, size_t bm,
+                     uint32_t *sorted, uint32_t *offsets, uint32_t *jobs) {
+    uint32_t acc = 0, jacc = 0;
+    for (size_t e = 0; e < experts; e++) {
+        uint32_t count = 0;
+        for (size_t a = 0; a < assignments; a++) count += ids[a] == e;
+        offsets[e] = acc;
+        uint32_t next = acc;
+        for (size_t a = 0; a < assignments; a++)
+            if (ids[a] == e) sorted[next++] = (uint32_t)a;
+        const uint32_t tiles = (uint32_t)((count + bm - 1) / bm);
+        for (uint32_t t = 0; t < tiles; t++) {
+            jobs[1 + 2 * (jacc + t)] = (uint32_t)e;
+            jobs[2 + 2 * (jacc + t)] = acc + t * (uint32_t)bm;
+        }
+        acc += count;
+        jacc += tiles;
+    }
+    offsets[experts] = acc;
+    jobs[0] = jacc;
+    return (int)jacc;
+}
+
 /* gpu/tests.rs:11-23 */
 float jvo_rng_next(uint64_t *state) {
     uint64_t x = *state;

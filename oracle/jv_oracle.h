@@ -86,6 +86,11 @@ int jvo_cpu_dequant_matmul(uint32_t type_id, const uint8_t *bytes, size_t n, siz
                            int threads);
 int jvo_omp_max_threads(void);
 
+/* ops::group (gpu/ops.rs:522-587): expert grouping of routed assignments (ids >= experts are
+ * not routed). Returns the job count. */
+int jvo_group_routes(const uint32_t *ids, size_t assignments, size_t experts, size_t bm,
+                     uint32_t *sorted, uint32_t *offsets, uint32_t *jobs);
+
 #ifdef __cplusplus
 }
 #endif

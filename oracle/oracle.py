@@ -57,6 +57,8 @@ def lib() -> C.CDLL:
         L.jvo_recipe_q6k.argtypes = [C.POINTER(U64), S, P]
         L.jvo_recipe_h16_vec.argtypes = [C.POINTER(U64), S, C.c_float, P]
         L.jvo_cpu_dequant_matmul.argtypes = [U32, P, S, S, P, S, P, P, C.c_int, C.c_int]
+        L.jvo_group_routes.argtypes = [P, S, S, S, P, P, P]
+        L.jvo_group_routes.restype = C.c_int
         L.jvo_omp_max_threads.restype = C.c_int
         _lib = L
     return _lib
@@ -151,6 +153,30 @@ def greedy(row: np.ndarray):
     if lib().jvo_greedy(_ptr(buf), row.size, C.byref(idx), C.byref(prob)):
         raise OracleError("invalid logits")
     return idx.value, prob.value
+
+
+def group_routes(ids: np.ndarray, experts: int, bm: int):
+    """ops::group (crates/jevons-gemma4-diffusion/src/gpu/ops.rs:522-587): (sorted, offsets,
+    jobs) with jobs[0] = job count and (expert, start) pairs after it."""
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    a = ids.size
+    max_jobs = (a + bm - 1) // bm + experts
+    sorted_ = np.zeros(max(a, 1), np.uint32)
+    offsets = np.zeros(experts + 1, np.uint32)
+    jobs = np.zeros(1 + 2 * max_jobs, np.uint32)
+    buf = ids if a else np.zeros(1, np.uint32)
+    lib().jvo_group_routes(_ptr(buf), a, experts, bm, _ptr(sorted_), _ptr(offsets), _ptr(jobs))
+    return sorted_[:offsets[experts]], offsets, jobs
+
+
+def grouped_product_f64(x: np.ndarray, w: np.ndarray, ids: np.ndarray, in_div: int, n: int):
+    """Reference of the grouped products: output row a = x[a // in_div] . W[ids[a] n : +n]^T in
+    f64 (the check of gpu/tests.rs:379-386), w the decoded [experts n, k] weights."""
+    ids = np.asarray(ids)
+    out = np.empty((ids.size, n), np.float64)
+    for a, e in enumerate(ids):
+        out[a] = matmul_f64(x[a // in_div][None, :], w[int(e) * n:(int(e) + 1) * n])[0]
+    return out
 
 
 class Rng:

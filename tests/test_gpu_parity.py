@@ -293,6 +293,82 @@ def test_q4k_prefill_gemm_m512_rows(gpu):
         assert torch.equal(o1, out[r0:r0 + 16]), r0
 
 
+# ------------------------------------------------------------------ expert-grouped products
+
+def _i32(a: np.ndarray):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).cuda()
+
+
+@pytest.mark.parametrize("experts,bm,a", [(4, 32, 42), (8, 16, 300), (128, 64, 2048), (3, 128, 5)])
+def test_group_routes_match_the_oracle(gpu, experts, bm, a):
+    """ops::group on the device equals its C restatement bitwise (ids >= experts included)."""
+    rng = np.random.default_rng(a + experts)
+    ids = rng.integers(0, experts + 1, a).astype(np.uint32)
+    g = jq.group_routes(gpu, _i32(ids), experts, bm)
+    sorted_, offsets, jobs = O.group_routes(ids, experts, bm)
+    njobs = int(jobs[0])
+    assert g.jobs.cpu().numpy().view(np.uint32)[:1 + 2 * njobs].tolist() == jobs[:1 + 2 * njobs].tolist()
+    assert g.offsets.cpu().numpy().view(np.uint32).tolist() == offsets.tolist()
+    assert g.ids.cpu().numpy().view(np.uint32)[:sorted_.size].tolist() == sorted_.tolist()
+
+
+def test_grouped_products_use_each_assignments_expert_weights(gpu):
+    """grouped_products_use_each_assignments_expert_weights (gpu/tests.rs:360-425): Q8_0
+    weights of 4 experts (n=128, k=256), 21 tokens routed to 2 experts each, every grouped tile
+    and split against the f64 product; tiles without split-K bitwise equal."""
+    tokens, top_k, experts, n, k = 21, 2, 4, 128, 256
+    rng = O.Rng(3)
+    raw = rng.recipe_q8_0(experts * n * k // 32)
+    w = jq.QMatrix.upload(gpu, jq.Q8_0, n, k, experts, raw)
+    dense = O.dequantize(jq.Q8_0, raw).reshape(experts * n, k)
+    x32 = rng.h16_vec(tokens * k, 1.0).reshape(tokens, k)
+    x = torch.from_numpy(x32.astype(np.float16)).cuda()
+    ids = np.array([(a * 7 + a // top_k) % experts for a in range(tokens * top_k)], np.uint32)
+    a = ids.size
+    want = O.grouped_product_f64(x32, dense, ids, top_k, n)
+    reference = None
+    scratch = jq.SplitScratch(gpu)
+    for bm in (32, 64):  # GroupPlan::ROW_TILES (gpu/tune.rs:104)
+        g = jq.group_routes(gpu, _i32(ids), experts, bm, in_div=top_k)
+        for bn in (64, 128):
+            for splits in (1, 2):
+                out = torch.zeros((a, n), dtype=torch.float32, device="cuda")
+                jq.matmul_grouped(gpu, x, w, g, out, bm, bn, splits, scratch)
+                got = out.cpu().numpy()
+                e = err(got, want)
+                assert e <= TOL, f"grouped {bm}x{bn}/{splits}: {e:.2e}"
+                if splits == 1:
+                    if reference is None:
+                        reference = got
+                    else:
+                        assert np.array_equal(reference, got), f"grouped {bm}x{bn}"
+    # the small-row grouped product (jobs of 16 rows)
+    g16 = jq.group_routes(gpu, _i32(ids), experts, 16, in_div=top_k)
+    out = torch.zeros((a, n), dtype=torch.float32, device="cuda")
+    jq.matvec_grouped(gpu, x, w, g16, out, 16)
+    assert err(out.cpu().numpy(), want) <= TOL
+
+
+@pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q5_0", jq.Q5_0)])
+def test_grouped_products_of_other_formats(gpu, name, type_id):
+    """Grouped products of 8 experts with uneven (and one empty) expert loads, bf16 rows, bf16
+    and f32 outputs."""
+    experts, n, k, top_k, tokens = 8, 128, 512, 2, 37
+    raw = synth.weights(type_id, 21, experts * n, k)
+    w = jq.QMatrix.upload(gpu, type_id, n, k, experts, raw)
+    dense = O.dequantize(type_id, raw).reshape(experts * n, k)
+    x, xv = activations("bf16", synth.normal_rows(22, tokens, k))
+    rng = np.random.default_rng(23)
+    ids = rng.choice([0, 1, 1, 2, 3, 3, 3, 5, 6, 7], tokens * top_k).astype(np.uint32)  # expert 4 empty
+    want = O.grouped_product_f64(xv, dense, ids, top_k, n)
+    g = jq.group_routes(gpu, _i32(ids), experts, 32, in_div=top_k)
+    for out_dtype in (torch.float32, torch.bfloat16):
+        out = torch.zeros((ids.size, n), dtype=out_dtype, device="cuda")
+        jq.matmul_grouped(gpu, x, w, g, out, 32, 128, 1, None)
+        e = err(out.float().cpu().numpy(), want)
+        assert e <= (TOL if out_dtype == torch.float32 else 8e-3), (out_dtype, e)
+
+
 # ------------------------------------------------------------------ lm_head argmax
 
 def test_argmax_follows_greedy(gpu):

@@ -310,3 +310,51 @@ def test_xorshift_fixture_generator(oracle):
         s ^= (s << 17) & 0xFFFFFFFFFFFFFFFF
         want = np.float32(np.float32(s >> 40) / np.float32(1 << 24) * np.float32(2.0) - np.float32(1.0))
         assert r.next() == want
+
+
+# ------------------------------------------------------------------ expert grouping
+
+def test_group_routes_hand_example(oracle):
+    """ops::group (gpu/ops.rs:522-587) on a small route list: experts in order, each expert's
+    assignments in assignment order, one (expert, start) job per bm-row tile."""
+    ids = np.array([2, 0, 2, 1, 0, 2, 2], np.uint32)
+    sorted_, offsets, jobs = oracle.group_routes(ids, 3, 2)
+    assert sorted_.tolist() == [1, 4, 3, 0, 2, 5, 6]
+    assert offsets.tolist() == [0, 2, 3, 7]
+    assert jobs[0] == 4
+    assert jobs[1:9].tolist() == [0, 0, 1, 2, 2, 3, 2, 5]
+
+
+@pytest.mark.parametrize("experts,bm,a", [(4, 32, 42), (8, 16, 100), (16, 64, 7), (5, 1, 30)])
+def test_group_routes_invariants(oracle, experts, bm, a):
+    """Brute-force properties of the grouping: every routed assignment appears once, experts
+    are contiguous and ascending, order is stable within an expert, the jobs tile every expert's
+    range with bm rows (the coverage check of gpu/tests.rs:340-357), ids >= experts are dropped."""
+    rng = np.random.default_rng(experts * 1000 + bm)
+    ids = rng.integers(0, experts + 1, a).astype(np.uint32)  # value `experts` is not routed
+    sorted_, offsets, jobs = oracle.group_routes(ids, experts, bm)
+    routed = [i for i in range(a) if ids[i] < experts]
+    assert sorted(sorted_.tolist()) == routed
+    for e in range(experts):
+        seg = sorted_[offsets[e]:offsets[e + 1]].tolist()
+        assert seg == [i for i in range(a) if ids[i] == e]
+    covered = 0
+    for j in range(jobs[0]):
+        e, start = int(jobs[1 + 2 * j]), int(jobs[2 + 2 * j])
+        assert offsets[e] <= start < offsets[e + 1] and (start - offsets[e]) % bm == 0
+        covered += min(int(offsets[e + 1]) - start, bm)
+    assert covered == len(routed)
+    assert jobs[0] == sum((int(offsets[e + 1] - offsets[e]) + bm - 1) // bm for e in range(experts))
+
+
+def test_grouped_product_reference(oracle):
+    """The f64 grouped product equals per-assignment products of the expert's rows."""
+    rng = np.random.default_rng(5)
+    experts, n, k, in_div = 3, 4, 8, 2
+    w = rng.standard_normal((experts * n, k)).astype(np.float32)
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    ids = np.array([1, 0, 2, 2, 0, 1])
+    got = oracle.grouped_product_f64(x, w, ids, in_div, n)
+    for a, e in enumerate(ids):
+        want = x[a // in_div].astype(np.float64) @ w[e * n:(e + 1) * n].astype(np.float64).T
+        assert np.allclose(got[a], want, rtol=0, atol=1e-12)
