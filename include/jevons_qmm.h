@@ -192,6 +192,17 @@ jv_status jv_f16_matmul(jv_ctx *ctx, const void *x, size_t m, size_t k, const vo
 jv_status jv_argmax_rows(jv_ctx *ctx, const float *logits, size_t rows, size_t n,
                          int32_t *index, jv_scratch *scratch, void *stream);
 
+/* Final-logit soft capping in place (softcap_logits, crates/jevons-gemma4-diffusion/src/gpu/
+ * ops.rs:1159-1168, kernel :750-758): x[i] = cap * tanh(x[i] / cap) for i < len; cap > 0. */
+jv_status jv_softcap_logits(jv_ctx *ctx, float *x, size_t len, float cap, void *stream);
+/* Candidate logits (pick, gpu/ops.rs:1133-1157, kernel pick_logits :589-634): for each of
+ * `count` device (row, token) pairs, out[p] = cap * tanh(x[row] . E[token] / cap), with E the
+ * weight rows of `table` (K = d, decoded exactly) and x [x_len / d][d]. A pair naming a row or
+ * token out of range gives NaN. */
+jv_status jv_pick_logits(jv_ctx *ctx, const void *x, jv_act act, size_t x_len,
+                         const jv_qmatrix *table, const uint32_t *pairs, size_t count, float *out,
+                         size_t out_len, float cap, void *stream);
+
 /* Exactness probes: decode rows [row0, row0 + rows) of `w` with the products' own device
  * decoder into FP32 (equal to quant::dequantize, quant.rs:83-101) or FP16 (the on-chip weight
  * tile, round-to-nearest-even of that FP32 value). Outputs are device [rows, k]. */

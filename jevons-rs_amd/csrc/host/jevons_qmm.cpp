@@ -1004,6 +1004,53 @@ jv_status jv_argmax_rows(jv_ctx *ctx, const float *logits, size_t rows, size_t n
     return launch(ctx, "jv_argmax_final", dim3((unsigned)rows), dim3(256), 0, stream, a2);
 }
 
+jv_status jv_softcap_logits(jv_ctx *ctx, float *x, size_t len, float cap, void *stream) {
+    jv_status st = use_device(ctx);
+    if (st != JV_OK) return st;
+    if (!(cap > 0.f) || !std::isfinite(cap)) return fail(JV_ERR_INVALID, "softcap %g must be positive", (double)cap);
+    if (len == 0) return JV_OK;
+    if (!x) return fail(JV_ERR_INVALID, "null buffer");
+    int64_t n = (int64_t)len;
+    void *args[] = {&x, &n, &cap};
+    return launch(ctx, "jv_softcap", dim3((unsigned)((len + 255) / 256)), dim3(256), 0, stream, args);
+}
+
+jv_status jv_pick_logits(jv_ctx *ctx, const void *x, jv_act act, size_t x_len,
+                         const jv_qmatrix *table, const uint32_t *pairs, size_t count, float *out,
+                         size_t out_len, float cap, void *stream) {
+    jv_status st = use_device(ctx);
+    if (st != JV_OK) return st;
+    if (!table) return fail(JV_ERR_INVALID, "null table");
+    if (act != JV_ACT_F16 && act != JV_ACT_BF16 && act != JV_ACT_F32)
+        return fail(JV_ERR_INVALID, "unknown activation type");
+    if (!(cap > 0.f) || !std::isfinite(cap)) return fail(JV_ERR_INVALID, "softcap %g must be positive", (double)cap);
+    if (out_len < count) return fail(JV_ERR_INVALID, "output holds %zu values, need %zu", out_len, count);
+    const size_t d = table->k;
+    if (x_len % d != 0) return fail(JV_ERR_INVALID, "activations (%zu) are not rows of %zu", x_len, d);
+    if (count == 0) return JV_OK;
+    if (!x || !pairs || !out) return fail(JV_ERR_INVALID, "null buffer");
+    if (count > (size_t)INT32_MAX || table->n * table->experts > (size_t)INT32_MAX ||
+        x_len / d > (size_t)INT32_MAX)
+        return fail(JV_ERR_INVALID, "pick_logits shape is too large");
+    PickParams p{};
+    p.x = x;
+    p.pairs = pairs;
+    p.wq = table->q;
+    p.wh = table->h;
+    p.wd = table->d;
+    p.out = out;
+    p.d = (int32_t)d;
+    p.act = (int32_t)act;
+    p.count = (int32_t)count;
+    p.x_rows = (int32_t)(x_len / d);
+    p.n = (int32_t)(table->n * table->experts);
+    p.cap = cap;
+    char name[40];
+    snprintf(name, sizeof name, "jv_pick_logits_%s", fmt_kernel_name(table->fmt));
+    void *args[] = {&p};
+    return launch(ctx, name, dim3((unsigned)count), dim3(256), 0, stream, args);
+}
+
 jv_status jv_dequant_rows_f32(jv_ctx *ctx, const jv_qmatrix *w, size_t row0, size_t rows,
                               float *out, void *stream) {
     return dequant_rows(ctx, w, row0, rows, out, 0, stream);

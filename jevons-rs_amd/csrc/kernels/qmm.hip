@@ -1647,6 +1647,66 @@ extern "C" __global__ __launch_bounds__(256) void jv_repack_q5_0(RepackParams p)
 // Row argmax with greedy's rule (crates/jevons-core/src/model.rs:207-219): the first maximum
 // wins; any non-finite value makes the row invalid (-1).
 // ---------------------------------------------------------------------------------------------
+// ---------------------------------------------------------------------------------------------
+// lm_head consumers (crates/jevons-gemma4-diffusion/src/gpu/ops.rs:589-634, :750-758).
+// ---------------------------------------------------------------------------------------------
+
+// In-place final-logit soft capping: x = cap tanh(x / cap).
+extern "C" __global__ __launch_bounds__(256) void jv_softcap(float *x, int64_t len, float cap) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < len) x[i] = cap * tanhf(x[i] / cap);
+}
+
+// One workgroup per (row, token) pair: thread i covers K unit i / 4 and lane group i % 4 of the
+// table row, decoding its weights exactly in FP32 (the F decoders), then the workgroup sums the
+// 256 partials in a fixed tree. A pair outside the activation rows or the table gives NaN.
+template <class F>
+__device__ __forceinline__ void pick_body(const PickParams &p) {
+    __shared__ float part[256];
+    const int pi = blockIdx.x;
+    const uint32_t row = p.pairs[2 * pi], token = p.pairs[2 * pi + 1];
+    const bool ok = row < (uint32_t)p.x_rows && token < (uint32_t)p.n;
+    float acc = 0.f;
+    if (ok) {
+        const int U = p.d / F::KU;
+        for (int i = threadIdx.x; i < U * 4; i += 256) {
+            const int u = i >> 2, g = i & 3;
+            typename F::Raw raw;
+            typename F::Prep pp;
+            F::load(raw, p.wq, p.wh, p.wd, p.d, (int)token, u, g);
+            F::prep(raw, pp, g);
+#pragma unroll
+            for (int s = 0; s < F::KU / 32; ++s) {
+                float v[8];
+                F::frag_f32(raw, pp, s, g, v);
+                const size_t c = (size_t)row * (size_t)p.d + (size_t)(u * F::KU + F::kidx(s, g));
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float xv = p.act == 0 ? h2f(((const uint16_t *)p.x)[c + e])
+                                   : p.act == 1 ? bf2f(((const uint16_t *)p.x)[c + e])
+                                                : ((const float *)p.x)[c + e];
+                    acc = __builtin_fmaf(v[e], xv, acc);
+                }
+            }
+        }
+    }
+    part[threadIdx.x] = acc;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) p.out[pi] = ok ? p.cap * tanhf(part[0] / p.cap) : __builtin_nanf("");
+}
+
+#define JV_PICK(NAME, F) \
+    extern "C" __global__ __launch_bounds__(256) void jv_pick_logits_##NAME(PickParams p) { pick_body<F>(p); }
+JV_PICK(q4k, FQ4K)
+JV_PICK(q6k, FQ6K)
+JV_PICK(q8_0, FQ8_0)
+JV_PICK(q5_0, FQ5_0)
+JV_PICK(f16, FF16)
+
 // Expert grouping (ops::group, crates/jevons-gemma4-diffusion/src/gpu/ops.rs:522-587), one
 // workgroup: sorted[] lists the assignments of expert 0, then 1, ... (each in assignment order),
 // offsets[e] is expert e's first sorted position (offsets[experts] = routed count), jobs[0] the

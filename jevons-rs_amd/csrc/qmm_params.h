@@ -65,4 +65,15 @@ struct RepackParams {
     int64_t chunks;      // work items (format-specific unit of the repack)
 };
 
+
+// Candidate logits (pick_logits): out[p] = cap tanh(x[row] . E[token] / cap), pair p = (row, token).
+struct PickParams {
+    const void *x;         // activations [x_rows][d], element type `act`
+    const uint32_t *pairs; // (row, token) pairs
+    const uint8_t *wq, *wh, *wd;  // the table's device regions
+    float *out;            // [count]
+    int32_t d, act, count, x_rows, n;
+    float cap;
+};
+
 #endif

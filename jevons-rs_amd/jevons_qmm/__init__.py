@@ -94,6 +94,8 @@ def lib() -> C.CDLL:
         "jv_group_routes": (I, [P, P, S, S, U32, P, P, P, S, P]),
         "jv_matmul_grouped": (I, [P, P, I, S, P, C.POINTER(jv_groups), P, I, S, U32, U32, U32, P, P]),
         "jv_matvec_grouped": (I, [P, P, I, S, P, C.POINTER(jv_groups), P, I, S, U32, P]),
+        "jv_softcap_logits": (I, [P, P, S, C.c_float, P]),
+        "jv_pick_logits": (I, [P, P, I, S, P, P, S, P, S, C.c_float, P]),
         "jv_last_error": (C.c_char_p, []),
     }
     for name, (res, args) in sigs.items():
@@ -389,6 +391,23 @@ def matvec_grouped(gpu: Gpu, x, w: QMatrix, g: Groups, out, mr: int, stream=None
     gc = g.c()
     _check(lib().jv_matvec_grouped(gpu.handle, _dev(x), _act(x), x.numel(), w.handle, C.byref(gc),
                                    _dev(out), _out(out), out.numel(), mr, _stream(stream)))
+
+
+def softcap_logits(gpu: Gpu, x, cap: float, stream=None) -> None:
+    """In-place x = cap tanh(x / cap) (softcap_logits, gpu/ops.rs:1159-1168)."""
+    _check(lib().jv_softcap_logits(gpu.handle, _dev(x), x.numel(), cap, _stream(stream)))
+
+
+def pick_logits(gpu: Gpu, x, table: QMatrix, pairs, cap: float, stream=None):
+    """Candidate logits cap tanh(x[row] . E[token] / cap) for device int32 (row, token) pairs
+    [count, 2] (pick, gpu/ops.rs:1133-1157)."""
+    import torch
+
+    count = pairs.numel() // 2
+    out = torch.empty(count, dtype=torch.float32, device=x.device)
+    _check(lib().jv_pick_logits(gpu.handle, _dev(x), _act(x), x.numel(), table.handle, _dev(pairs),
+                                count, _dev(out), out.numel(), cap, _stream(stream)))
+    return out
 
 
 def argmax_rows(gpu: Gpu, logits, scratch: SplitScratch, stream=None):

@@ -179,6 +179,19 @@ def grouped_product_f64(x: np.ndarray, w: np.ndarray, ids: np.ndarray, in_div: i
     return out
 
 
+def softcap(v, cap: float):
+    """Final-logit soft capping cap tanh(v / cap) in f64 (gpu/ops.rs:750-758)."""
+    return cap * np.tanh(np.asarray(v, np.float64) / cap)
+
+
+def pick_logits_f64(x: np.ndarray, table: np.ndarray, pairs: np.ndarray, cap: float) -> np.ndarray:
+    """pick_logits (gpu/ops.rs:589-634) in f64: softcap(x[row] . E[token]) per (row, token) pair,
+    table the decoded [tokens, d] rows."""
+    pairs = np.asarray(pairs).reshape(-1, 2)
+    dots = np.array([x[r].astype(np.float64) @ table[t].astype(np.float64) for r, t in pairs])
+    return softcap(dots, cap)
+
+
 class Rng:
     """xorshift64 fixture generator of crates/jevons-gemma4-diffusion/src/gpu/tests.rs:11-23."""
 

@@ -416,6 +416,39 @@ def test_q6k_lm_head_logits_and_argmax(gpu, m):
         assert idx[r] == O.greedy(out[r].cpu().numpy())[0]
 
 
+# ------------------------------------------------------------------ lm_head consumers
+
+@pytest.mark.parametrize("name,type_id", [("q6k", jq.Q6K), ("q4k", jq.Q4K), ("q8_0", jq.Q8_0)])
+def test_pick_logits_match_the_oracle(gpu, name, type_id):
+    """pick_logits (gpu/ops.rs:589-634): softcap(x[row] . E[token]) for (row, token) pairs of a
+    1024-token table, against the f64 oracle; out-of-range pairs give NaN."""
+    tokens, d, rows, cap = 1024, 768, 6, 30.0
+    raw = synth.weights(type_id, 31, tokens, d)
+    table = jq.QMatrix.upload(gpu, type_id, tokens, d, 1, raw)
+    dense = O.dequantize(type_id, raw).reshape(tokens, d)
+    x, xv = activations("f16", synth.normal_rows(32, rows, d))
+    rng = np.random.default_rng(33)
+    pairs = np.stack([rng.integers(0, rows, 300), rng.integers(0, tokens, 300)], axis=1).astype(np.uint32)
+    pairs[7] = pairs[3]  # duplicates
+    got = jq.pick_logits(gpu, x, table, torch.from_numpy(pairs.view(np.int32)).cuda(), cap).cpu().numpy()
+    want = O.pick_logits_f64(xv, dense, pairs, cap)
+    assert np.max(np.abs(got - want)) <= TOL * np.max(np.abs(want))
+    assert got[7] == got[3]
+    bad = np.array([[rows, 0], [0, tokens], [1, 5]], np.uint32)
+    got = jq.pick_logits(gpu, x, table, torch.from_numpy(bad.view(np.int32)).cuda(), cap).cpu().numpy()
+    assert np.isnan(got[0]) and np.isnan(got[1]) and np.isfinite(got[2])
+
+
+def test_softcap_logits(gpu):
+    """softcap_logits (gpu/ops.rs:1159-1168) in place against the f64 restatement."""
+    v = torch.from_numpy(np.random.default_rng(34).standard_normal(100003).astype(np.float32) * 40).cuda()
+    want = O.softcap(v.cpu().numpy(), 30.0)
+    jq.softcap_logits(gpu, v, 30.0)
+    assert np.max(np.abs(v.cpu().numpy() - want)) <= 4e-6 * 30.0
+    with pytest.raises(jq.JvError):
+        jq.softcap_logits(gpu, v, 0.0)
+
+
 # ------------------------------------------------------------------ Burn operator
 
 @pytest.mark.parametrize("m,n,k", [(32, 64, 256), (32, 4160, 512), (64, 256, 1024), (512, 384, 512),

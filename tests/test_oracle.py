@@ -358,3 +358,15 @@ def test_grouped_product_reference(oracle):
     for a, e in enumerate(ids):
         want = x[a // in_div].astype(np.float64) @ w[e * n:(e + 1) * n].astype(np.float64).T
         assert np.allclose(got[a], want, rtol=0, atol=1e-12)
+
+
+def test_softcap_is_a_smooth_clamp(oracle):
+    """cap tanh(v / cap) (gpu/ops.rs:750-758): odd, zero at zero, identity to first order for
+    |v| << cap, bounded by cap and approaching it."""
+    cap = 30.0
+    v = np.array([-1e6, -90.0, -1e-3, 0.0, 1e-3, 15.0, 90.0, 1e6])
+    got = oracle.softcap(v, cap)
+    assert got[3] == 0.0
+    assert np.allclose(got, -oracle.softcap(-v, cap), rtol=0, atol=0)
+    assert abs(got[4] - 1e-3) < 1e-12 and np.all(np.abs(got) <= cap)
+    assert cap - got[-1] < 1e-9 and abs(got[5] - 30.0 * np.tanh(0.5)) < 1e-12
