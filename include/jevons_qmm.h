@@ -211,6 +211,57 @@ jv_status jv_dequant_rows_f32(jv_ctx *ctx, const jv_qmatrix *w, size_t row0, siz
 jv_status jv_dequant_rows_f16(jv_ctx *ctx, const jv_qmatrix *w, size_t row0, size_t rows,
                               uint16_t *out, void *stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Launch-plan tuner and its table (crates/jevons-gemma4-diffusion/src/gpu/tune.rs). Plans are
+ * keyed by (format, n, k, row bucket, row invariance) and, for grouped products, (format, n, k,
+ * experts, row bucket); a bucket b = max(next power of two of m, 4) serves m in (b/2, b]
+ * (tune.rs:73-76). Lookups fall back to jv_plan_auto (grouped: bm 32, bn 128 or 64); a stored
+ * row-invariant plan is used only if it splits no K (tune.rs:162-174, :485-487).
+ * ------------------------------------------------------------------------------------------ */
+typedef struct jv_tuner jv_tuner;
+/* Row bucket of m (tune.rs:73-76). */
+size_t jv_tune_bucket(size_t m);
+/* Buckets tuned for row counts up to `max` from `min` (buckets, tune.rs:489-497): min, 2 min, ...
+ * up to bucket(max) and at most 1024. Writes up to `cap` of them; returns their count. */
+size_t jv_tune_buckets(size_t min, size_t max, size_t *out, size_t cap);
+/* The measured plan rule (pick, tune.rs:556-566): index of the fastest of n timed candidates,
+ * unless it beats the candidate whose id is `baseline` by less than 5%; -1 if n == 0. */
+int jv_tune_pick(const double *times, const uint32_t *ids, size_t n, uint32_t baseline);
+/* Tuner for this context's device (Tuner::new, tune.rs:132-151): loads `path` (NULL: nothing
+ * stored) when its profile line matches the device. */
+jv_status jv_tuner_new(jv_ctx *ctx, const char *path, jv_tuner **out);
+/* A table without a device (lookups and storage only), for the given profile line. */
+jv_status jv_tuner_open_table(const char *profile, const char *path, jv_tuner **out);
+void jv_tuner_free(jv_tuner *t);
+const char *jv_tuner_profile(const jv_tuner *t);
+size_t jv_tuner_entries(const jv_tuner *t);
+/* Stored dense plan for (fmt, n, k, bucket(m), row_invariant); 1 if present. */
+int jv_tuner_lookup_dense(const jv_tuner *t, uint32_t fmt, size_t n, size_t k, size_t m,
+                          int row_invariant, jv_plan *plan);
+void jv_tuner_insert_dense(jv_tuner *t, uint32_t fmt, size_t n, size_t k, size_t bucket,
+                           int row_invariant, jv_plan plan);
+void jv_tuner_insert_grouped(jv_tuner *t, uint32_t fmt, size_t n, size_t k, size_t experts,
+                             size_t bucket, uint32_t bm, uint32_t bn);
+/* Tuner::dense (tune.rs:162-174) and Tuner::grouped (tune.rs:177-190). */
+jv_plan jv_tuner_dense(const jv_tuner *t, const jv_qmatrix *w, size_t m, int row_invariant);
+jv_status jv_tuner_grouped(const jv_tuner *t, const jv_qmatrix *w, size_t rows, uint32_t *bm,
+                           uint32_t *bn);
+/* Measures the candidate plans for matrices `ws` of one shape at m = bucket rows (tune_dense,
+ * tune.rs:229-268); x, out are scratch of at least m*k and m*n values. *added = 1 when a plan
+ * was stored. */
+jv_status jv_tuner_tune_dense(jv_tuner *t, const jv_qmatrix *const *ws, size_t nws, size_t m,
+                              int row_invariant, const void *x, jv_act act, size_t x_len,
+                              void *out, size_t out_len, jv_scratch *scratch, int *added);
+/* Measures the grouped tiles for `rows` tokens routed to top_k experts each (tune_grouped,
+ * tune.rs:270-343); route_ids, sorted, offsets, jobs are device scratch (route_capacity ids). */
+jv_status jv_tuner_tune_grouped(jv_tuner *t, const jv_qmatrix *const *ws, size_t nws, size_t rows,
+                                size_t top_k, const void *x, jv_act act, size_t x_len, void *out,
+                                size_t out_len, uint32_t *route_ids, size_t route_capacity,
+                                uint32_t *sorted, uint32_t *offsets, uint32_t *jobs,
+                                size_t jobs_len, jv_scratch *scratch, int *added);
+/* Writes the table (Tuner::save, tune.rs:413-444): the profile line, then sorted entries. */
+jv_status jv_tuner_save(const jv_tuner *t);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char *jv_last_error(void);
 

@@ -563,6 +563,10 @@ jv_status dequant_rows(jv_ctx *ctx, const jv_qmatrix *w, size_t row0, size_t row
 
 extern "C" {
 
+// Error channel for the library's other translation units (the plan tuner); not part of the
+// public header.
+jv_status jv_internal_fail(jv_status st, const char *msg) { return fail(st, "%s", msg); }
+
 jv_status jv_type_block(uint32_t ggml_type, uint32_t *elems, uint32_t *bytes) {
     uint32_t e, b;
     if (!type_block(ggml_type, &e, &b)) return fail(JV_ERR_UNSUPPORTED, "unsupported tensor type");
@@ -781,7 +785,9 @@ jv_plan jv_plan_heuristic(const jv_qmatrix *w, size_t m, int row_invariant, size
 // workgroup, then (outside prefill) split-K until the grid fills the device.
 jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
     if (!w) return jv_plan{0, 0, 0};
-    if (m <= 16) return jv_plan{0, 64, 1};
+    // The small-row kernel keeps a row's bits independent of m but not equal to the tile
+    // kernels' bits, so row-invariant (prefill) products always take tiles (gemm.rs:989-994).
+    if (m <= 16 && !row_invariant) return jv_plan{0, 64, 1};
     const size_t cus = w->ctx ? (size_t)std::max(1, w->ctx->info.compute_units) : 256;
     const size_t cols = w->n * w->experts;
     // Pipelined tiles (whole K, so row invariant): 256 x 128 when that gives about one workgroup

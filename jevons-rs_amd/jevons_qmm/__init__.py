@@ -96,6 +96,23 @@ def lib() -> C.CDLL:
         "jv_matvec_grouped": (I, [P, P, I, S, P, C.POINTER(jv_groups), P, I, S, U32, P]),
         "jv_softcap_logits": (I, [P, P, S, C.c_float, P]),
         "jv_pick_logits": (I, [P, P, I, S, P, P, S, P, S, C.c_float, P]),
+        "jv_tune_bucket": (S, [S]),
+        "jv_tune_buckets": (S, [S, S, C.POINTER(S), S]),
+        "jv_tune_pick": (I, [C.POINTER(C.c_double), C.POINTER(U32), S, U32]),
+        "jv_tuner_new": (I, [P, C.c_char_p, PP]),
+        "jv_tuner_open_table": (I, [C.c_char_p, C.c_char_p, PP]),
+        "jv_tuner_free": (None, [P]),
+        "jv_tuner_profile": (C.c_char_p, [P]),
+        "jv_tuner_entries": (S, [P]),
+        "jv_tuner_lookup_dense": (I, [P, U32, S, S, S, I, C.POINTER(jv_plan)]),
+        "jv_tuner_insert_dense": (None, [P, U32, S, S, S, I, jv_plan]),
+        "jv_tuner_insert_grouped": (None, [P, U32, S, S, S, S, U32, U32]),
+        "jv_tuner_dense": (jv_plan, [P, P, S, I]),
+        "jv_tuner_grouped": (I, [P, P, S, C.POINTER(U32), C.POINTER(U32)]),
+        "jv_tuner_tune_dense": (I, [P, C.POINTER(P), S, S, I, P, I, S, P, S, P, C.POINTER(I)]),
+        "jv_tuner_tune_grouped": (I, [P, C.POINTER(P), S, S, S, P, I, S, P, S, P, S, P, P, P, S, P,
+                                      C.POINTER(I)]),
+        "jv_tuner_save": (I, [P]),
         "jv_last_error": (C.c_char_p, []),
     }
     for name, (res, args) in sigs.items():
@@ -391,6 +408,99 @@ def matvec_grouped(gpu: Gpu, x, w: QMatrix, g: Groups, out, mr: int, stream=None
     gc = g.c()
     _check(lib().jv_matvec_grouped(gpu.handle, _dev(x), _act(x), x.numel(), w.handle, C.byref(gc),
                                    _dev(out), _out(out), out.numel(), mr, _stream(stream)))
+
+
+def tune_bucket(m: int) -> int:
+    """Row bucket (bucket, tune.rs:73-76)."""
+    return lib().jv_tune_bucket(m)
+
+
+def tune_buckets(lo: int, hi: int) -> list[int]:
+    """Buckets tuned for row counts up to hi (buckets, tune.rs:489-497)."""
+    n = lib().jv_tune_buckets(lo, hi, None, 0)
+    out = (C.c_size_t * max(n, 1))()
+    lib().jv_tune_buckets(lo, hi, out, n)
+    return list(out[:n])
+
+
+def tune_pick(times, ids, baseline: int) -> int | None:
+    """Index of the chosen candidate (pick, tune.rs:556-566), None for no candidates."""
+    n = len(times)
+    t = (C.c_double * max(n, 1))(*times)
+    i = (C.c_uint32 * max(n, 1))(*ids)
+    r = lib().jv_tune_pick(t, i, n, baseline)
+    return None if r < 0 else r
+
+
+class Tuner:
+    """Launch-plan tuner and its table (Tuner, crates/jevons-gemma4-diffusion/src/gpu/tune.rs)."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    @staticmethod
+    def new(gpu: "Gpu", path: str | None) -> "Tuner":
+        h = C.c_void_p()
+        _check(lib().jv_tuner_new(gpu.handle, path.encode() if path else None, C.byref(h)))
+        return Tuner(h)
+
+    @staticmethod
+    def open_table(profile: str, path: str | None) -> "Tuner":
+        h = C.c_void_p()
+        _check(lib().jv_tuner_open_table(profile.encode(), path.encode() if path else None, C.byref(h)))
+        return Tuner(h)
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            lib().jv_tuner_free(self.handle)
+            self.handle = None
+
+    @property
+    def profile(self) -> str:
+        return lib().jv_tuner_profile(self.handle).decode()
+
+    def entries(self) -> int:
+        return lib().jv_tuner_entries(self.handle)
+
+    def lookup_dense(self, fmt: int, n: int, k: int, m: int, row_invariant: bool):
+        p = jv_plan()
+        if lib().jv_tuner_lookup_dense(self.handle, fmt, n, k, m, int(row_invariant), C.byref(p)):
+            return Plan(p.bm, p.bn, p.splits)
+        return None
+
+    def insert_dense(self, fmt, n, k, bucket, row_invariant, plan: "Plan"):
+        lib().jv_tuner_insert_dense(self.handle, fmt, n, k, bucket, int(row_invariant), plan.c())
+
+    def insert_grouped(self, fmt, n, k, experts, bucket, bm, bn):
+        lib().jv_tuner_insert_grouped(self.handle, fmt, n, k, experts, bucket, bm, bn)
+
+    def dense(self, w: "QMatrix", m: int, row_invariant: bool) -> "Plan":
+        p = lib().jv_tuner_dense(self.handle, w.handle, m, int(row_invariant))
+        return Plan(p.bm, p.bn, p.splits)
+
+    def grouped(self, w: "QMatrix", rows: int):
+        bm, bn = C.c_uint32(), C.c_uint32()
+        _check(lib().jv_tuner_grouped(self.handle, w.handle, rows, C.byref(bm), C.byref(bn)))
+        return bm.value, bn.value
+
+    def tune_dense(self, ws, m: int, row_invariant: bool, x, out, scratch) -> bool:
+        arr = (C.c_void_p * len(ws))(*[w.handle for w in ws])
+        added = C.c_int()
+        _check(lib().jv_tuner_tune_dense(self.handle, arr, len(ws), m, int(row_invariant), _dev(x), _act(x),
+                                         x.numel(), _dev(out), out.numel(), _sh(scratch), C.byref(added)))
+        return bool(added.value)
+
+    def tune_grouped(self, ws, rows: int, top_k: int, x, out, route_ids, sorted_, offsets, jobs, scratch) -> bool:
+        arr = (C.c_void_p * len(ws))(*[w.handle for w in ws])
+        added = C.c_int()
+        _check(lib().jv_tuner_tune_grouped(self.handle, arr, len(ws), rows, top_k, _dev(x), _act(x), x.numel(),
+                                           _dev(out), out.numel(), _dev(route_ids), route_ids.numel(),
+                                           _dev(sorted_), _dev(offsets), _dev(jobs), jobs.numel(), _sh(scratch),
+                                           C.byref(added)))
+        return bool(added.value)
+
+    def save(self) -> None:
+        _check(lib().jv_tuner_save(self.handle))
 
 
 def softcap_logits(gpu: Gpu, x, cap: float, stream=None) -> None:

@@ -449,6 +449,51 @@ def test_softcap_logits(gpu):
         jq.softcap_logits(gpu, v, 0.0)
 
 
+# ------------------------------------------------------------------ plan tuner
+
+def test_tuner_measures_stores_and_serves_plans(gpu, tmp_path):
+    """Tuner::tune / dense / grouped (gpu/tune.rs:196-343): measured plans are valid for their
+    bucket, row-invariant ones split no K, the table reloads for this device, and products with
+    the tuned plans match the oracle."""
+    path = str(tmp_path / "plans.txt")
+    t = jq.Tuner.new(gpu, path)
+    n, k = 256, 512
+    ws = [make_matrix(gpu, jq.Q4K, n, k, seed=s)[0] for s in (40, 41)]
+    raw = synth.weights(jq.Q4K, 40, n, k)
+    scratch = jq.SplitScratch(gpu)
+    x, xv = activations("bf16", synth.normal_rows(42, 64, k))
+    out = torch.empty((64, n), dtype=torch.float32, device="cuda")
+    for m, ri in ((64, True), (8, False), (4, True)):
+        assert t.tune_dense(ws, m, ri, x, out, scratch)
+        p = t.dense(ws[0], m, ri)
+        assert p.valid_for(ws[0], m)
+        if ri:
+            assert p.bm > 0 and p.splits == 1
+        o = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        jq.matmul_plan(gpu, x[:m].contiguous(), m, ws[0], o, scratch, p)
+        assert err(o.cpu().numpy(), oracle_product(jq.Q4K, raw, n, k, xv[:m])) <= TOL
+    # grouped tiles for 8 experts, 16 tokens x top-2
+    experts, top_k, rows = 8, 2, 16
+    wg = jq.QMatrix.upload(gpu, jq.Q8_0, n, k, experts, synth.weights(jq.Q8_0, 43, experts * n, k))
+    cap = rows * top_k
+    max_jobs = cap // 32 + experts
+    route = torch.zeros(cap, dtype=torch.int32, device="cuda")
+    sorted_ = torch.zeros(cap, dtype=torch.int32, device="cuda")
+    offsets = torch.zeros(experts + 1, dtype=torch.int32, device="cuda")
+    jobs = torch.zeros(1 + 2 * (cap + experts), dtype=torch.int32, device="cuda")
+    xg, _ = activations("f16", synth.normal_rows(44, cap, k))
+    og = torch.empty((cap, n), dtype=torch.float32, device="cuda")
+    assert t.tune_grouped([wg], rows, top_k, xg, og, route, sorted_, offsets, jobs, scratch)
+    bm, bn = t.grouped(wg, rows)
+    assert bm in (32, 64) and bn in (64, 128) and max_jobs > 0
+    t.save()
+    u = jq.Tuner.new(gpu, path)
+    assert u.entries() == t.entries() == 4
+    for m, ri in ((64, True), (8, False), (4, True)):
+        assert u.dense(ws[0], m, ri) == t.dense(ws[0], m, ri)
+    assert u.grouped(wg, rows) == (bm, bn)
+
+
 # ------------------------------------------------------------------ Burn operator
 
 @pytest.mark.parametrize("m,n,k", [(32, 64, 256), (32, 4160, 512), (64, 256, 1024), (512, 384, 512),
@@ -517,6 +562,11 @@ def test_plan_rules_follow_the_reference(gpu):
     assert not jq.Plan(0, 128, 2).valid_for(w, 4)
     assert jq.Plan(128, 128, 8).valid_for(w, 4) and not jq.Plan(128, 128, 9).valid_for(w, 4)
     assert not jq.Plan(128, 128, 0).valid_for(w, 4)
+    # the library's own plan: small-row kernel only when rows may differ from the tiles' bits
+    assert jq.Plan.auto(w, 4, row_invariant=False).bm == 0
+    for m in (1, 4, 16, 70):
+        p = jq.Plan.auto(w, m, row_invariant=True)
+        assert p.bm > 0 and p.splits == 1 and p.valid_for(w, m), (m, p)
     # the gfx950 256 x 128 tile: any format, whole K in 256-element blocks, no split-K
     assert jq.Plan(256, 128, 1).valid_for(w, 512)
     w320 = jq.QMatrix.upload(gpu, jq.Q8_0, 256, 320, 1, synth.weights(jq.Q8_0, 1, 256, 320))
