@@ -262,6 +262,31 @@ jv_status jv_tuner_tune_grouped(jv_tuner *t, const jv_qmatrix *const *ws, size_t
 /* Writes the table (Tuner::save, tune.rs:413-444): the profile line, then sorted entries. */
 jv_status jv_tuner_save(const jv_tuner *t);
 
+/* ---------------------------------------------------------------------------------------------
+ * GGUF v2/v3 reader (Gguf, crates/jevons-formats/src/gguf.rs:163-372): validated metadata,
+ * tensor directory (absolute offsets, byte sizes of the block-encoded types) and bounded reads;
+ * errors carry the reference's messages ("Invalid GGUF file: ...", "Missing tensor ...").
+ * ------------------------------------------------------------------------------------------ */
+typedef struct jv_gguf jv_gguf;
+jv_status jv_gguf_open(const char *path, jv_gguf **out);  /* Gguf::open (gguf.rs:234-321) */
+void jv_gguf_close(jv_gguf *g);
+size_t jv_gguf_tensor_count(const jv_gguf *g);
+/* TensorInfo (gguf.rs:146-155): dims in GGML order (dims[0] = row length), unused dims = 1;
+ * bytes = 0 for types without a block size. */
+jv_status jv_gguf_tensor_info(const jv_gguf *g, size_t index, const char **name,
+                              uint32_t *ggml_type, uint32_t *n_dims, uint64_t dims[4],
+                              uint64_t *offset, uint64_t *bytes);
+jv_status jv_gguf_find(const jv_gguf *g, const char *name, size_t *index);  /* Gguf::tensor */
+jv_status jv_gguf_u64(const jv_gguf *g, const char *key, uint64_t *out);    /* Gguf::u64 */
+jv_status jv_gguf_f32(const jv_gguf *g, const char *key, float *out);       /* Gguf::f32 */
+jv_status jv_gguf_str(const jv_gguf *g, const char *key, const char **out);
+/* Gguf::read / read_range (gguf.rs:338-362): bytes [start, start + len) of a tensor of a
+ * decodable type into host memory. */
+jv_status jv_gguf_read(const jv_gguf *g, size_t index, uint64_t start, uint64_t len, void *dst);
+/* Reads a [k, n] or [k, n, experts] tensor and uploads it (QMatrix::upload, gemm.rs:822-841;
+ * the loader step of model.rs:302-351). */
+jv_status jv_gguf_upload(jv_ctx *ctx, const jv_gguf *g, const char *name, jv_qmatrix **out);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char *jv_last_error(void);
 

@@ -22,6 +22,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 KERNEL_SRC = os.path.join(HERE, "csrc", "kernels", "qmm.hip")
 HOST_SRC = os.path.join(HERE, "csrc", "host", "jevons_qmm.cpp")
 TUNE_SRC = os.path.join(HERE, "csrc", "host", "tune.cpp")
+GGUF_SRC = os.path.join(HERE, "csrc", "host", "gguf.cpp")
 
 # Packed FP32 VALU instructions are disabled for all device code.
 HIPCC_FLAGS = [
@@ -39,7 +40,7 @@ def host_cmd(out: str = SO) -> list[str]:
     return [
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
         "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROOT, "include"),
-        "-I", os.path.join(ROCM, "include"), HOST_SRC, TUNE_SRC,
+        "-I", os.path.join(ROCM, "include"), HOST_SRC, TUNE_SRC, GGUF_SRC,
         "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
         "-o", out,
     ]

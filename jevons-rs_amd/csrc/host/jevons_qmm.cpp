@@ -430,6 +430,8 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
     if (!x || !out) return fail(JV_ERR_INVALID, "null activation or output buffer");
     if (((uintptr_t)x & 15u) != 0) return fail(JV_ERR_INVALID, "activations must be 16-byte aligned");
 
+    // Products use expert 0's rows of an expert stack (the first n rows), as the reference's
+    // ungrouped kernels do (wrow = expert * n + col with expert 0, gemm.rs:463-464).
     // Small-row Q4_K, Q6_K and Q8_0 kernels. Up to 8 tiles (16 rows) per compute unit: one
     // workgroup per one or two tiles (two from m = 3 on for Q4_K and Q8_0, which halves the
     // activation staging per weight byte). Wider matrices: persistent workgroups that stage the
@@ -445,7 +447,7 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         const int ku = q8 ? 64 : 256;  // K per item
         const int xg = q6 ? 16 : 32;   // columns per activation sum
         const int U = (int)(w->k / ku);
-        const int T = (int)(w->n * w->experts / 16);
+        const int T = (int)(w->n / 16);
         const int umax = (U + waves - 1) / waves;
         const bool persist = T >= 8 * cus;
         const int tw = persist || q6 || m <= 2 ? 1 : 2;
@@ -464,10 +466,10 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
             p.out = out;
             p.wq = w->q;
             p.M = (int32_t)m;
-            p.N = (int32_t)(w->n * w->experts);
+            p.N = (int32_t)(w->n);
             p.K = (int32_t)w->k;
             p.ldx = (int32_t)w->k;
-            p.ldo = (int32_t)(w->n * w->experts);
+            p.ldo = (int32_t)(w->n);
             p.act = (int32_t)act;
             p.out_type = (int32_t)out_type;
             p.splits = 1;
@@ -521,15 +523,15 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         gp.wd = w->d;
         gp.out = out;
         gp.M = (int32_t)m;
-        gp.N = (int32_t)(w->n * w->experts);
+        gp.N = (int32_t)(w->n);
         gp.K = (int32_t)w->k;
-        gp.ldo = (int32_t)(w->n * w->experts);
+        gp.ldo = (int32_t)(w->n);
         gp.out_type = (int32_t)out_type;
         void *gargs[] = {&gp};
         char name[40];
         snprintf(name, sizeof name, "jv_gemm_%s_%ux%u", fmt_kernel_name(w->fmt), plan.bm, plan.bn);
         const unsigned waves = plan.bm >= 128 ? 8 : 4;
-        return launch(ctx, name, dim3((unsigned)(w->n * w->experts / plan.bn), (unsigned)(mtiles * 16 / plan.bm)),
+        return launch(ctx, name, dim3((unsigned)(w->n / plan.bn), (unsigned)(mtiles * 16 / plan.bm)),
                       dim3(64 * waves), 4 * (plan.bm + plan.bn) / 16 * 1024, stream, gargs);
     }
     return launch_tiles(ctx, x, act, m, w, out, out_type, scratch, plan, stream, nullptr);
@@ -789,7 +791,7 @@ jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
     // kernels' bits, so row-invariant (prefill) products always take tiles (gemm.rs:989-994).
     if (m <= 16 && !row_invariant) return jv_plan{0, 64, 1};
     const size_t cus = w->ctx ? (size_t)std::max(1, w->ctx->info.compute_units) : 256;
-    const size_t cols = w->n * w->experts;
+    const size_t cols = w->n;
     // Pipelined tiles (whole K, so row invariant): 256 x 128 when that gives about one workgroup
     // per compute unit (each weight decoded once per 256 rows); otherwise 64 x 64, which keeps
     // more compute units busy on narrow matrices. Fewer rows take the generic tiles.

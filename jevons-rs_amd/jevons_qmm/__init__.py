@@ -113,6 +113,17 @@ def lib() -> C.CDLL:
         "jv_tuner_tune_grouped": (I, [P, C.POINTER(P), S, S, S, P, I, S, P, S, P, S, P, P, P, S, P,
                                       C.POINTER(I)]),
         "jv_tuner_save": (I, [P]),
+        "jv_gguf_open": (I, [C.c_char_p, PP]),
+        "jv_gguf_close": (None, [P]),
+        "jv_gguf_tensor_count": (S, [P]),
+        "jv_gguf_tensor_info": (I, [P, S, C.POINTER(C.c_char_p), C.POINTER(U32), C.POINTER(U32),
+                                    C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+        "jv_gguf_find": (I, [P, C.c_char_p, C.POINTER(S)]),
+        "jv_gguf_u64": (I, [P, C.c_char_p, C.POINTER(C.c_uint64)]),
+        "jv_gguf_f32": (I, [P, C.c_char_p, C.POINTER(C.c_float)]),
+        "jv_gguf_str": (I, [P, C.c_char_p, C.POINTER(C.c_char_p)]),
+        "jv_gguf_read": (I, [P, S, C.c_uint64, C.c_uint64, P]),
+        "jv_gguf_upload": (I, [P, P, C.c_char_p, PP]),
         "jv_last_error": (C.c_char_p, []),
     }
     for name, (res, args) in sigs.items():
@@ -501,6 +512,63 @@ class Tuner:
 
     def save(self) -> None:
         _check(lib().jv_tuner_save(self.handle))
+
+
+class Gguf:
+    """GGUF v2/v3 file (Gguf, crates/jevons-formats/src/gguf.rs:163-372)."""
+
+    def __init__(self, path: str):
+        self.handle = None
+        h = C.c_void_p()
+        _check(lib().jv_gguf_open(path.encode(), C.byref(h)))
+        self.handle = h
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            lib().jv_gguf_close(self.handle)
+            self.handle = None
+
+    def tensors(self) -> dict:
+        """name -> (ggml_type, dims, absolute offset, bytes)."""
+        out = {}
+        for i in range(lib().jv_gguf_tensor_count(self.handle)):
+            name, t, nd = C.c_char_p(), C.c_uint32(), C.c_uint32()
+            dims, off, nb = (C.c_uint64 * 4)(), C.c_uint64(), C.c_uint64()
+            _check(lib().jv_gguf_tensor_info(self.handle, i, C.byref(name), C.byref(t), C.byref(nd), dims,
+                                             C.byref(off), C.byref(nb)))
+            out[name.value.decode()] = (t.value, list(dims[:nd.value]), off.value, nb.value)
+        return out
+
+    def u64(self, key: str) -> int:
+        v = C.c_uint64()
+        _check(lib().jv_gguf_u64(self.handle, key.encode(), C.byref(v)))
+        return v.value
+
+    def f32(self, key: str) -> float:
+        v = C.c_float()
+        _check(lib().jv_gguf_f32(self.handle, key.encode(), C.byref(v)))
+        return v.value
+
+    def str(self, key: str) -> str:
+        v = C.c_char_p()
+        _check(lib().jv_gguf_str(self.handle, key.encode(), C.byref(v)))
+        return v.value.decode()
+
+    def read(self, name: str, start: int = 0, length: int | None = None):
+        import numpy as np
+
+        idx = C.c_size_t()
+        _check(lib().jv_gguf_find(self.handle, name.encode(), C.byref(idx)))
+        if length is None:
+            length = self.tensors()[name][3] - start
+        buf = np.empty(max(length, 1), np.uint8)
+        _check(lib().jv_gguf_read(self.handle, idx.value, start, length, buf.ctypes.data))
+        return buf[:length]
+
+    def upload(self, gpu: Gpu, name: str) -> "QMatrix":
+        h = C.c_void_p()
+        _check(lib().jv_gguf_upload(gpu.handle, self.handle, name.encode(), C.byref(h)))
+        return QMatrix(h)
 
 
 def softcap_logits(gpu: Gpu, x, cap: float, stream=None) -> None:

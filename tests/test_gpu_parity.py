@@ -449,6 +449,41 @@ def test_softcap_logits(gpu):
         jq.softcap_logits(gpu, v, 0.0)
 
 
+# ------------------------------------------------------------------ GGUF -> device
+
+def test_gguf_tensors_upload_unchanged(gpu, tmp_path):
+    """The loader step (model.rs:302-351): a [k, n] Q4_K tensor and a [k, n, experts] Q8_0 stack
+    read from a GGUF file give the same products as the same bytes uploaded directly."""
+    from helpers import write_gguf
+
+    n, k, experts = 128, 512, 3
+    q4 = synth.weights(jq.Q4K, 51, n, k)
+    q8 = synth.weights(jq.Q8_0, 52, experts * n, k)
+    path = str(tmp_path / "w.gguf")
+    write_gguf(path, {"general.architecture": (8, "gemma4")},
+               [("a.weight", [k, n], 12, q4), ("b.weight", [k, n, experts], 8, q8)])
+    g = jq.Gguf(path)
+    x, _ = activations("bf16", synth.normal_rows(53, 5, k))
+    for name, raw, kind, e in (("a.weight", q4, jq.Q4K, 1), ("b.weight", q8, jq.Q8_0, experts)):
+        wf = g.upload(gpu, name)
+        wd = jq.QMatrix.upload(gpu, kind, n, k, e, raw)
+        assert wf.bytes() == wd.bytes()
+        a = jq.dequant_rows(gpu, wf, 0, n * e).cpu().numpy()
+        b = jq.dequant_rows(gpu, wd, 0, n * e).cpu().numpy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        o1 = torch.empty((5, n), dtype=torch.float32, device="cuda")
+        o2 = torch.empty((5, n), dtype=torch.float32, device="cuda")
+        jq.matmul(gpu, x, 5, wf, o1)
+        jq.matmul(gpu, x, 5, wd, o2)
+        assert torch.equal(o1, o2)
+        # ungrouped products of an expert stack use expert 0's rows, as the reference's kernels do
+        per_row = raw.size // (n * e)
+        w0 = jq.QMatrix.upload(gpu, kind, n, k, 1, raw[:n * per_row].copy())
+        o3 = torch.empty((5, n), dtype=torch.float32, device="cuda")
+        jq.matmul(gpu, x, 5, w0, o3)
+        assert torch.equal(o1, o3)
+
+
 # ------------------------------------------------------------------ plan tuner
 
 def test_tuner_measures_stores_and_serves_plans(gpu, tmp_path):
