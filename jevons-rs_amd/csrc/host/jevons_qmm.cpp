@@ -794,8 +794,11 @@ jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
     const size_t cols = w->n;
     // Pipelined tiles (whole K, so row invariant): 256 x 128 when that gives about one workgroup
     // per compute unit (each weight decoded once per 256 rows); otherwise 64 x 64, which keeps
-    // more compute units busy on narrow matrices. Fewer rows take the generic tiles.
-    if (w->k % 256 == 0 && m >= 48) {
+    // more compute units busy on narrow matrices and wastes the least on a few rows (at m = 32
+    // of the Q6_K vocabulary projection it beats the 32-row generic tiles by 1.6x). A few rows
+    // of a narrow matrix outside prefill keep the generic tiles, whose split-K fills the device.
+    const size_t tiles64 = (cols / 64) * ((m + 63) / 64);
+    if (w->k % 256 == 0 && (m >= 48 || row_invariant || tiles64 >= cus)) {
         if (cols % 128 == 0 && m >= 128 && ((m + 255) / 256) * (cols / 128) * 16 >= cus * 15)
             return jv_plan{256, 128, 1};
         if (cols % 64 == 0) return jv_plan{64, 64, 1};
