@@ -105,11 +105,12 @@ def pmc_child():
     mats = [jq.QMatrix.upload_device(gpu, jq.Q4K, n, k, 1, raw_dev) for _ in range(copies)]
     x8 = synth.normal_rows(21, 8, k)
     xb = torch.from_numpy(synth.to_bf16(x8).view(np.int16).copy()).view(torch.bfloat16).cuda()
+    scratch = jq.SplitScratch(gpu)
     for m in GEMV_MS:
         xm = xb[:m].contiguous()
         out = torch.empty((m, n), dtype=torch.float32, device="cuda")
         for r in range(20):
-            jq.matmul(gpu, xm, m, mats[r % copies], out)
+            jq.matmul(gpu, xm, m, mats[r % copies], out, scratch)
         torch.cuda.synchronize()
     srcs = [torch.empty(raw.size, dtype=torch.uint8, device="cuda") for _ in range(copies)]
     dst = torch.empty(raw.size, dtype=torch.uint8, device="cuda")
@@ -355,10 +356,11 @@ def main():
     xb = torch.from_numpy(synth.to_bf16(x8).view(np.int16).copy()).view(torch.bfloat16).cuda()
     xs = {m: xb[:m].contiguous() for m in ms}
     outs = {m: torch.empty((m, n), dtype=torch.float32, device="cuda") for m in ms}
+    scratch = jq.SplitScratch(gpu)  # split-K partials (SplitScratch, gemm.rs:1041-1065)
 
     def gemv_step(i):
         for j, m in enumerate(ms):
-            jq.matmul(gpu, xs[m], m, mats[(3 * i + j) % copies], outs[m])
+            jq.matmul(gpu, xs[m], m, mats[(3 * i + j) % copies], outs[m], scratch)
 
     gemv_step(0)
     torch.cuda.synchronize()
@@ -375,7 +377,7 @@ def main():
 
     # per-kernel durations (M = 1, 4, 8)
     reps = 100
-    kt = [kernel_time_ms(lambda r, m=m: jq.matmul(gpu, xs[m], m, mats[r % copies], outs[m]), reps)
+    kt = [kernel_time_ms(lambda r, m=m: jq.matmul(gpu, xs[m], m, mats[r % copies], outs[m], scratch), reps)
           for m in ms]
     per_m = {m: {"kernel_us": round(t * 1e3, 3), "weight_GBps": round(wbytes / (t * 1e-3) / 1e9, 1)}
              for m, t in zip(ms, kt)}

@@ -161,6 +161,27 @@ struct jv_scratch {
 
 namespace {
 
+// Every scratch allocation starts with the split-K small-row kernels' tile counters (zeroed when
+// allocated, a multiple of 16 after every launch); partial buffers of all uses follow them.
+constexpr size_t kCounterTiles = 65536;
+constexpr size_t kCounterBytes = kCounterTiles * 4;
+
+// Grows `s` to hold `payload` bytes after the counters and returns the payload's address.
+jv_status scratch_reserve(jv_scratch *s, size_t payload, void **out) {
+    const size_t need = kCounterBytes + payload;
+    if (s->bytes < need) {
+        if (s->buf) JV_HIP(hipFree(s->buf));
+        s->buf = nullptr;
+        s->bytes = 0;
+        JV_HIP(hipMalloc(&s->buf, need));
+        JV_HIP(hipMemset(s->buf, 0, kCounterBytes));
+        JV_HIP(hipDeviceSynchronize());
+        s->bytes = need;
+    }
+    *out = (uint8_t *)s->buf + kCounterBytes;
+    return JV_OK;
+}
+
 jv_status get_fn(jv_ctx *ctx, const std::string &name, hipFunction_t *out) {
     auto it = ctx->fns.find(name);
     if (it != ctx->fns.end()) {
@@ -384,15 +405,10 @@ jv_status launch_tiles(jv_ctx *ctx, const void *x, jv_act act, size_t m, const j
     }
     if (splits > 1) {
         if (!scratch) return fail(JV_ERR_INVALID, "split-K plans need a scratch buffer");
-        const size_t need = (size_t)splits * m * w->n * 4;
-        if (scratch->bytes < need) {
-            if (scratch->buf) JV_HIP(hipFree(scratch->buf));
-            scratch->buf = nullptr;
-            scratch->bytes = 0;
-            JV_HIP(hipMalloc(&scratch->buf, need));
-            scratch->bytes = need;
-        }
-        p.out = scratch->buf;
+        void *partials = nullptr;
+        st = scratch_reserve(scratch, (size_t)splits * m * w->n * 4, &partials);
+        if (st != JV_OK) return st;
+        p.out = partials;
     } else {
         p.out = out;
     }
@@ -403,7 +419,7 @@ jv_status launch_tiles(jv_ctx *ctx, const void *x, jv_act act, size_t m, const j
     void *args[] = {&p};
     st = launch(ctx, name, grid, dim3(256), lds, stream, args);
     if (st != JV_OK || splits == 1) return st;
-    const void *part = scratch->buf;
+    const void *part = p.out;
     int64_t len = (int64_t)(m * w->n);
     int sp = splits, ot = (int)out_type;
     void *rargs[] = {&part, &out, &len, &sp, &ot};
@@ -434,9 +450,9 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
     // ungrouped kernels do (wrow = expert * n + col with expert 0, gemm.rs:463-464).
     // Small-row Q4_K, Q6_K and Q8_0 kernels. Up to 8 tiles (16 rows) per compute unit: one
     // workgroup per one or two tiles (two from m = 3 on for Q4_K and Q8_0, which halves the
-    // activation staging per weight byte). Wider matrices: persistent workgroups that stage the
-    // activations once and stream a range of tiles. All variants sum each output element the
-    // same way, so every output row is the same for any m.
+    // activation staging per weight byte), or split-K workgroups (below). Wider matrices:
+    // persistent workgroups that stage the activations once and stream a range of tiles. All
+    // variants sum each output element the same way, so every output row is the same for any m.
     if (plan.bm == 0 && (w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
         w->n * w->experts * w->k < (1ull << 32)) {
         const bool q8 = w->fmt == JV_FMT_Q8_0, q6 = w->fmt == JV_FMT_Q6K;
@@ -460,7 +476,20 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
                              ~(size_t)15;
         const size_t lds = persist ? stage * waves + 2 * 2 * (size_t)waves * 1024
                                    : std::max(stage, (size_t)tw * 1024) * waves;
-        if (lds <= ctx->info.lds_bytes) {
+        // Split-K workgroups (with a scratch buffer): `waves` tiles x one of `waves` K slices
+        // each, the slice staged once per workgroup (`stage` bytes of LDS). Their reduction
+        // through device memory costs a few microseconds at the end, so they serve the products
+        // whose per-tile staging is the larger cost: Q4_K and Q6_K above 8 rows, and any K too
+        // long for the per-tile kernels' LDS.
+        // JV_QMV_SPLIT=0 or 1 overrides the choice where both kernels apply (tests, tuning).
+        const char *force = getenv("JV_QMV_SPLIT");
+        const bool split_ok = scratch && !persist && U >= waves && (size_t)T <= kCounterTiles &&
+                              stage <= ctx->info.lds_bytes;
+        const bool split = split_ok && (lds > ctx->info.lds_bytes ||
+                                        (force && (force[0] == '0' || force[0] == '1')
+                                             ? force[0] == '1'
+                                             : !q8 && m > 8));
+        if (lds <= ctx->info.lds_bytes || split) {
             QmmParams p{};
             p.x = x;
             p.out = out;
@@ -475,6 +504,17 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
             p.splits = 1;
             void *args[] = {&p};
             char name[32];
+            if (split) {
+                void *partials = nullptr;
+                st = scratch_reserve(scratch, (size_t)waves * m * w->n * 4, &partials);
+                if (st != JV_OK) return st;
+                p.part = (float *)partials;
+                p.counters = (uint32_t *)scratch->buf;
+                const int groups = (T + waves - 1) / waves;
+                const int gp = (groups + 7) & ~7;  // the kernel's XCD mapping pads groups to 8
+                snprintf(name, sizeof name, "jv_qmvs_%s_m%d", fname, mv);
+                return launch(ctx, name, dim3((unsigned)(waves * gp)), dim3(64 * waves), stage, stream, args);
+            }
             if (persist) {
                 snprintf(name, sizeof name, "jv_qmvp_%s_m%d", fname, mv);
                 hipFunction_t f;
@@ -994,15 +1034,11 @@ jv_status jv_argmax_rows(jv_ctx *ctx, const float *logits, size_t rows, size_t n
     const int chunk = 8192;
     int chunks = (int)((n + chunk - 1) / chunk);
     const size_t need = std::max<size_t>(rows * (size_t)chunks * 8, 16);
-    if (scratch->bytes < need) {
-        if (scratch->buf) JV_HIP(hipFree(scratch->buf));
-        scratch->buf = nullptr;
-        scratch->bytes = 0;
-        JV_HIP(hipMalloc(&scratch->buf, need));
-        scratch->bytes = need;
-    }
-    float *pval = (float *)scratch->buf;
-    int *pidx = (int *)((uint8_t *)scratch->buf + rows * (size_t)chunks * 4);
+    void *partials = nullptr;
+    st = scratch_reserve(scratch, need, &partials);
+    if (st != JV_OK) return st;
+    float *pval = (float *)partials;
+    int *pidx = (int *)((uint8_t *)partials + rows * (size_t)chunks * 4);
     if (chunks > 0) {
         int64_t nn = (int64_t)n;
         int ch = chunk;

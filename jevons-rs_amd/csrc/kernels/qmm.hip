@@ -633,6 +633,85 @@ __device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int 
     if (!issued) after();
 }
 
+// stage_wave_cols with the work shared by the W waves of a workgroup: the 8-element chunks are
+// numbered row-major and wave w takes the 64-chunk batches w, w + W, w + 2W, ... Each chunk's
+// values and sums are computed as in stage_wave_cols.
+template <int ACT, int XB, int XG, int W, class After>
+__device__ __forceinline__ void stage_group_cols(const QmmParams &p, int c0, int ncols, _Float16 *xs,
+                                                 int stride, float *Xs, int xstride, int lane,
+                                                 int wave, After after) {
+    constexpr int EPL = ACT == 2 ? 4 : 8;  // elements per 16-byte load
+    constexpr int LPC = 8 / EPL;           // loads per 8-element chunk
+    constexpr int XC = XB / LPC;           // chunks held per lane at once
+    const int per_row = ncols >> 3;
+    const int total = p.M * per_row;  // 8-element chunks; a multiple of 4 (ncols % 32 == 0)
+    bool issued = false;
+    for (int i0 = 64 * wave; i0 < total; i0 += XC * 64 * W) {
+        uint4 raw[XC][LPC];
+        const int nq = min(XC, (total - i0 + 64 * W - 1) / (64 * W));  // uniform: batches holding real chunks
+#pragma unroll
+        for (int q = 0; q < XC; ++q) {
+            if (q >= nq) break;
+            const int i = min(i0 + q * 64 * W + lane, total - 1);
+            const int r = i / per_row;
+            const int c8 = i - r * per_row;
+            const size_t src = (size_t)r * (size_t)p.ldx + (size_t)(c0 + 8 * c8);
+#pragma unroll
+            for (int hh = 0; hh < LPC; ++hh) {
+                if (ACT == 2)
+                    raw[q][hh] = *(const uint4 *)((const float *)p.x + src + 4 * hh);
+                else
+                    raw[q][hh] = *(const uint4 *)((const uint16_t *)p.x + src);
+            }
+        }
+        if (!issued) {
+            after();
+            issued = true;
+        }
+#pragma unroll
+        for (int q = 0; q < XC; ++q) {
+            if (q >= nq) break;
+            const int i = i0 + q * 64 * W + lane;
+            float part = 0.f;
+            int r = 0, c8 = 0;
+            if (i < total) {
+                r = i / per_row;
+                c8 = i - r * per_row;
+                float v[8];
+                if (ACT == 2) {
+#pragma unroll
+                    for (int hh = 0; hh < LPC; ++hh) {
+                        v[4 * hh + 0] = __builtin_bit_cast(float, raw[q][hh].x);
+                        v[4 * hh + 1] = __builtin_bit_cast(float, raw[q][hh].y);
+                        v[4 * hh + 2] = __builtin_bit_cast(float, raw[q][hh].z);
+                        v[4 * hh + 3] = __builtin_bit_cast(float, raw[q][hh].w);
+                    }
+                } else {
+                    const uint32_t w[4] = {raw[q][0].x, raw[q][0].y, raw[q][0].z, raw[q][0].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[2 * e] = ACT == 0 ? h2f(w[e]) : bf2f(w[e]);
+                        v[2 * e + 1] = ACT == 0 ? h2f(w[e] >> 16) : bf2f(w[e] >> 16);
+                    }
+                }
+                f16x8 h;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = (_Float16)v[e];
+                // FP32 sum of the FP16 values, two per dot-product step
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    part = __builtin_amdgcn_fdot2(f16x2{h[2 * e], h[2 * e + 1]}, f16x2{1.0f16, 1.0f16}, part, false);
+                *(f16x8 *)(xs + r * stride + 8 * c8) = h;
+            }
+            // lanes 4q..4q+3 hold the four 8-element chunks of one 32-element sub-block
+            part += __shfl_xor(part, 1);
+            if (XG == 32) part += __shfl_xor(part, 2);
+            if (i < total && (c8 & (XG / 8 - 1)) == 0) Xs[r * xstride + c8 / (XG / 8)] = part;
+        }
+    }
+    if (!issued) after();
+}
+
 // One block against activations staged in LDS, with the scale arithmetic regrouped to cut
 // vector ALU work (the kernel is bound by it once the loads are in flight):
 //   out += d * (sum_even s_j S_j + (sum_odd s_j S_j) / 16) - sum_j (1024 d s'_j + dmin m_j) X_j,
@@ -1082,6 +1161,120 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
     }
 }
 
+// Split-K variant of qmv_body: a workgroup of W waves owns W tiles and one of W K slices, slice
+// s being the units [s U / W, (s + 1) U / W) that wave s covers in qmv_body. Its waves stage
+// the slice's activation columns together, so each workgroup reads 1/W of the activations
+// instead of all of them. Wave w computes tile w's partial over the slice (qmv_body's wave s
+// chain for that tile), stores it to p.part and counts it on the tile's counter; the wave
+// that completes the count adds the W partials in slice order and writes the outputs. That is qmv_body's sum, term for term, so every variant gives the same bits.
+// Counters advance by 16 per launch (16 / W per wave) and so stay a multiple of 16 between
+// launches for any W dividing 16. Block b maps to slice b / GP and tile group b % GP, GP =
+// the group count rounded up to a multiple of 8, so that the slices of a group share an XCD.
+template <class G, int W, int P, int MV, int XB>
+__device__ __forceinline__ void qmvs_body(const QmmParams &p) {
+    static_assert(16 % W == 0, "W must divide 16");
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4;
+    const int r16 = lane & 15;
+    const int U = p.K / G::KU;
+    const int T = p.N >> 4;
+    const int groups = (T + W - 1) / W;
+    const int gp = (groups + 7) & ~7;
+    const int s = blockIdx.x / gp;
+    const int tg = blockIdx.x - s * gp;
+    if (tg >= groups) return;  // workgroup-uniform: padding of the XCD mapping
+    const int u0 = s * U / W;
+    const int nu = (s + 1) * U / W - u0;
+    const int umax = (U + W - 1) / W;
+    const int stride = umax * G::KU + kLdsPad;
+    const int xstride = umax * (G::KU / G::XG);
+    _Float16 *xs = (_Float16 *)lds;
+    float *Xs = (float *)((uint8_t *)lds + p.M * stride * 2);
+    _Float16 *zrow = (_Float16 *)((uint8_t *)lds + p.M * stride * 2 + p.M * xstride * 4);
+    const int tile = tg * W + wave;
+    const bool live = tile < T;  // wave-uniform
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (nu > 0) {  // workgroup-uniform
+        typename G::Item buf[P];
+        auto load_item = [&](typename G::Item &dst, int idx) {
+            G::load(dst, p, tile, u0 + min(idx, nu - 1), g, r16);
+        };
+        auto issue = [&] {
+            if (live) {
+#pragma unroll
+                for (int j = 0; j < P; ++j) load_item(buf[j], j);
+            }
+        };
+        const int c0 = u0 * G::KU, nc = nu * G::KU;
+        if (G::kZeroRow)
+            for (int i = (int)threadIdx.x; i < stride / 8; i += 64 * W) *(f16x8 *)(zrow + 8 * i) = f16x8{};
+        if (p.act == 0)
+            stage_group_cols<0, XB, G::XG, W>(p, c0, nc, xs, stride, Xs, xstride, lane, wave, issue);
+        else if (p.act == 1)
+            stage_group_cols<1, XB, G::XG, W>(p, c0, nc, xs, stride, Xs, xstride, lane, wave, issue);
+        else
+            stage_group_cols<2, XB, G::XG, W>(p, c0, nc, xs, stride, Xs, xstride, lane, wave, issue);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_barrier();
+        if (live) {
+            const int arow = min(r16, p.M - 1);  // rows >= M feed output rows that are never stored
+            const _Float16 *xrow = xs + arow * stride;
+            const float *Xrow = Xs + arow * xstride;
+            const typename G::Lane lc = G::lane_consts(g);
+            for (int i0 = 0; i0 < nu; i0 += P) {
+#pragma unroll
+                for (int j = 0; j < P; ++j) {
+                    const int idx = i0 + j;
+                    if (idx < nu) G::template block<MV>(buf[j], xrow, zrow, Xrow, idx, g, lc, acc);
+                    if (i0 + P < nu) load_item(buf[j], idx + P);
+                }
+            }
+        }
+    }
+    if (!live) return;
+    // the lane index again from mbcnt, so that it is not held in a register across the loop
+    const int ln = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    const int lg = ln >> 4;
+    const int col = tile * 16 + (ln & 15);
+    const size_t plane = (size_t)p.M * (size_t)p.N;
+    // Partials are written and read at device scope (sc1: through to the level every compute
+    // unit sees, no cache-wide write-back or invalidate); the store acknowledgements are awaited
+    // before the count, and the reads are issued only after the count completes.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * lg + i;
+        if (m < p.M)
+            __hip_atomic_store(p.part + (size_t)s * plane + (size_t)m * p.N + col, acc[i],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    uint32_t old = 0;
+    if (ln == 0)
+        old = __hip_atomic_fetch_add(p.counters + tile, 16u / W, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (((old + 16u / W) & 15u) != 0) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * lg + i;
+        if (m < p.M) {
+            float sum = 0.f;
+            for (int t = 0; t < W; ++t) {
+                const float v = t == s ? acc[i]
+                                       : __hip_atomic_load(p.part + (size_t)t * plane + (size_t)m * p.N + col,
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                sum = t == 0 ? v : sum + v;
+            }
+            const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
+            if (p.out_type == 0)
+                ((float *)p.out)[o] = sum;
+            else
+                ((uint16_t *)p.out)[o] = (uint16_t)f2bf(sum);
+        }
+    }
+}
+
 }  // namespace
 
 // One-tile workgroups run four per compute unit (8 waves per SIMD, at most 64 VGPRs); the
@@ -1132,6 +1325,22 @@ JV_QMV8(1, 2, 4)
 JV_QMV8(2, 1, 4)
 JV_QMV8(2, 2, 4)
 JV_QMV8(2, 4, 8)
+
+// Split-K kernels: W tiles x one K slice per workgroup (activation staging shared by the waves).
+#define JV_QMVS(NAME, G, W, P, MV, XB, WPE)                                                  \
+    extern "C" __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) \
+    void jv_qmvs_##NAME##_m##MV(QmmParams p) {                                               \
+        qmvs_body<G, W, P, MV, XB>(p);                                                       \
+    }
+JV_QMVS(q4k, GQ4K, 8, 2, 1, 2, 8)
+JV_QMVS(q4k, GQ4K, 8, 2, 2, 2, 8)
+JV_QMVS(q4k, GQ4K, 8, 2, 4, 8, 4)
+JV_QMVS(q6k, GQ6K, 8, 2, 1, 2, 4)
+JV_QMVS(q6k, GQ6K, 8, 2, 2, 4, 4)
+JV_QMVS(q6k, GQ6K, 8, 2, 4, 4, 3)
+JV_QMVS(q8_0, GQ8_0, 16, 4, 1, 2, 4)
+JV_QMVS(q8_0, GQ8_0, 16, 4, 2, 4, 4)
+JV_QMVS(q8_0, GQ8_0, 16, 4, 4, 8, 4)
 
 // ---------------------------------------------------------------------------------------------
 // Entry points (looked up by name with hipModuleGetFunction).

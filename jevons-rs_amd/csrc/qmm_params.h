@@ -24,6 +24,10 @@ struct QmmParams {
     // input row ids[s] / in_div and writes output row ids[s]; weight rows start at e * N.
     const uint32_t *ids, *offsets, *jobs;
     int32_t grouped, in_div, rows_cap;
+    // Split-K small-row kernels: FP32 slice partials [slices][M][N] and one arrival counter per
+    // 16-row tile (kept at a multiple of 16 between launches).
+    float *part;
+    uint32_t *counters;
 };
 
 // Decode probe: rows [row0, row0 + rows) of a weight matrix into [rows][K].

@@ -189,6 +189,82 @@ def test_small_row_product_of_wide_matrices(gpu, name, type_id):
         assert np.array_equal(out.cpu().numpy(), rows[m][:, :64]), m
 
 
+@pytest.mark.parametrize("name,type_id,k", [("q4k", jq.Q4K, 3840), ("q4k", jq.Q4K, 2048),
+                                             ("q6k", jq.Q6K, 3840), ("q8_0", jq.Q8_0, 4096)])
+def test_split_k_small_row_products_equal_the_per_tile_kernels(gpu, monkeypatch, name, type_id, k):
+    """Split-K small-row workgroups (W tiles x one of W K slices, the last slice to arrive adding
+    the partials; taken here for every m with JV_QMV_SPLIT=1 and a scratch buffer). Their outputs
+    must be bitwise those of the per-tile kernels (jv_matvec, no scratch) for every m, match the
+    f64 oracle, and keep every row independent of m. 576 rows: a last tile group that is only
+    partly filled."""
+    monkeypatch.setenv("JV_QMV_SPLIT", "1")
+    n = 576
+    w, raw = make_matrix(gpu, type_id, n, k, seed=13)
+    scratch = jq.SplitScratch(gpu)
+    x_all = synth.normal_rows(61, 16, k)
+    rows = {}
+    for m in (1, 2, 3, 8, 16):
+        x, xv = activations("bf16", x_all[:m])
+        say(name, "split", n, k, "m", m)
+        split = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matmul(gpu, x, m, w, split, scratch)
+        tile = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matvec(gpu, x, m, w, tile)
+        got = split.cpu().numpy()
+        assert np.array_equal(got, tile.cpu().numpy()), f"m={m}: split-K differs from per-tile"
+        e = err(got, oracle_product(type_id, raw, n, k, xv))
+        assert e <= TOL, f"m={m}: normalized error {e:.2e}"
+        rows[m] = got
+    for m in (1, 2, 3, 8):
+        assert np.array_equal(rows[m], rows[16][:m]), m
+    # the same scratch again, after a split-K tiled product and a product of another format
+    # (a different wave count per tile): the tile counters are left at a multiple of 16
+    other, _ = make_matrix(gpu, jq.Q8_0 if type_id != jq.Q8_0 else jq.Q4K, 256, 4096, seed=3)
+    xo, _ = activations("bf16", synth.normal_rows(5, 4, 4096))
+    jq.matmul(gpu, xo, 4, other, torch.empty((4, 256), dtype=torch.float32, device="cuda"), scratch)
+    jq.matmul_plan(gpu, xo, 4, other, torch.empty((4, 256), dtype=torch.float32, device="cuda"),
+                   scratch, jq.Plan(32, 64, 4))
+    for act in ("bf16", "f16", "f32"):
+        x, _ = activations(act, x_all[:8])
+        a = torch.empty((8, n), dtype=torch.float32, device="cuda")
+        b = torch.empty((8, n), dtype=torch.float32, device="cuda")
+        for _ in range(2):
+            jq.matmul(gpu, x, 8, w, a, scratch)
+        jq.matvec(gpu, x, 8, w, b)
+        assert np.array_equal(a.cpu().numpy(), b.cpu().numpy()), act
+    x, _ = activations("bf16", x_all[:3])
+    a16 = torch.empty((3, n), dtype=torch.bfloat16, device="cuda")
+    b16 = torch.empty((3, n), dtype=torch.bfloat16, device="cuda")
+    jq.matmul(gpu, x, 3, w, a16, scratch)
+    jq.matvec(gpu, x, 3, w, b16)
+    assert torch.equal(a16, b16)
+
+
+@pytest.mark.parametrize("name,type_id,k", [("q6k", jq.Q6K, 15360), ("q4k", jq.Q4K, 15360),
+                                             ("q8_0", jq.Q8_0, 16384)])
+def test_small_row_products_of_long_rows(gpu, name, type_id, k):
+    """K too long for the per-tile kernels' per-wave staging at larger m (the down projection,
+    K = 15360): the library takes the split-K workgroups, which stage one K slice per
+    workgroup. Outputs against the f64 oracle; rows independent of m across the switch from
+    per-tile (small m) to split-K kernels."""
+    n = 576
+    w, raw = make_matrix(gpu, type_id, n, k, seed=17)
+    scratch = jq.SplitScratch(gpu)
+    x_all = synth.normal_rows(71, 16, k)
+    rows = {}
+    for m in (1, 4, 8, 16):
+        x, xv = activations("bf16", x_all[:m])
+        say(name, "long rows", n, k, "m", m)
+        out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matmul(gpu, x, m, w, out, scratch)
+        got = out.cpu().numpy()
+        e = err(got, oracle_product(type_id, raw, n, k, xv))
+        assert e <= TOL, f"m={m}: normalized error {e:.2e}"
+        rows[m] = got
+    for m in (1, 4, 8):
+        assert np.array_equal(rows[m], rows[16][:m]), m
+
+
 def test_reference_dense_plan_recipe(gpu):
     """every_tunable_dense_plan_matches_reference_and_tiles_are_row_invariant
     (gpu/tests.rs:427-480): Q8_0 N=256 K=512, FP16 rows, every reference plan."""
@@ -268,6 +344,10 @@ def test_q4k_decode_gemv_full_shape(gpu, m):
     e = err(got, want)
     say("normalized error", e)
     assert e <= TOL
+    # split-K workgroups (with a scratch buffer): the same bits
+    split = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    jq.matmul(gpu, x, m, w, split, jq.SplitScratch(gpu))
+    assert np.array_equal(split.cpu().numpy(), got)
 
 
 def test_q4k_prefill_gemm_m512_rows(gpu):
