@@ -569,10 +569,17 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         gp.out_type = (int32_t)out_type;
         void *gargs[] = {&gp};
         char name[40];
-        snprintf(name, sizeof name, "jv_gemm_%s_%ux%u", fmt_kernel_name(w->fmt), plan.bm, plan.bn);
-        const unsigned waves = plan.bm >= 128 ? 8 : 4;
+        // Q6_K and Q8_0 256 x 128 tiles run on 4 waves of 64 x 128 (same bits as the 8-wave
+        // tile; JV_GEMM_W4=0 selects the 8-wave one).
+        const char *w4env = getenv("JV_GEMM_W4");
+        const bool w4 = plan.bm == 256 && (w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
+                        !(w4env && w4env[0] == '0');
+        snprintf(name, sizeof name, "jv_gemm_%s_%ux%u%s", fmt_kernel_name(w->fmt), plan.bm, plan.bn,
+                 w4 ? "w4" : "");
+        const unsigned waves = w4 ? 4 : (plan.bm >= 128 ? 8 : 4);
+        const size_t glds = 4 * ((w4 ? 0 : plan.bm) + plan.bn) / 16 * 1024;
         return launch(ctx, name, dim3((unsigned)(w->n / plan.bn), (unsigned)(mtiles * 16 / plan.bm)),
-                      dim3(64 * waves), 4 * (plan.bm + plan.bn) / 16 * 1024, stream, gargs);
+                      dim3(64 * waves), glds, stream, gargs);
     }
     return launch_tiles(ctx, x, act, m, w, out, out_type, scratch, plan, stream, nullptr);
 }

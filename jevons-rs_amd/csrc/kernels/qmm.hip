@@ -1571,7 +1571,11 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     constexpr int AS = MT / WN;  // activation fragments a wave stages per stage (own m slots)
     constexpr int BS = NT / WM;  // weight fragments a wave decodes per stage (own n slots)
     constexpr int UPS = 8 / D::SPU;  // K units per 8 stages
-    constexpr int BUF = (TM + TN) * 1024;
+    // Activation fragments go through LDS only when several waves share an m-tile (WN > 1);
+    // with WN = 1 every wave loads all of its own fragments and LDS holds only the weights.
+    constexpr bool ASH = AS < MT;
+    constexpr int AOFF = ASH ? TM * 1024 : 0;  // weight fragments' offset in a buffer
+    constexpr int BUF = AOFF + TN * 1024;
     static_assert(AS * W == TM && BS * W == TN && AS >= 1 && BS >= 1, "tile split");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63;
@@ -1610,9 +1614,11 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     // four LDS buffers, stage st in buffer st % 4 (a compile-time index in the unrolled loop)
     auto buf_of = [&](int st) __attribute__((always_inline)) { return smem + (st & 3) * BUF + lo16; };
     auto store_a = [&](const u32x4 *src, int st) __attribute__((always_inline)) {
-        uint8_t *base = buf_of(st);
+        if constexpr (ASH) {
+            uint8_t *base = buf_of(st);
 #pragma unroll
-        for (int i = 0; i < AS; ++i) *(u32x4 *)(base + m_of(i) * 1024) = src[i];
+            for (int i = 0; i < AS; ++i) *(u32x4 *)(base + m_of(i) * 1024) = src[i];
+        }
     };
     // raw weights of the 8 stages from stage 8 b on (K units UPS b .. UPS b + UPS - 1)
     auto load_w = [&](typename D::Raw (*dst)[BS], int b) __attribute__((always_inline)) {
@@ -1630,7 +1636,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     };
     auto store_b = [&](const f16x8 *v, int st) __attribute__((always_inline)) {
 #pragma unroll
-        for (int k = 0; k < BS; ++k) *(f16x8 *)(buf_of(st) + TM * 1024 + n_of(k) * 1024) = v[k];
+        for (int k = 0; k < BS; ++k) *(f16x8 *)(buf_of(st) + AOFF + n_of(k) * 1024) = v[k];
     };
     // the fragments of stage st this wave does not hold
     auto read_other = [&](f16x8 *fa, f16x8 *fb, int st) __attribute__((always_inline)) {
@@ -1638,7 +1644,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 #pragma unroll
         for (int i = 0; i < MT - AS; ++i) fa[i] = *(const f16x8 *)(base + m_of(AS + i) * 1024);
 #pragma unroll
-        for (int k = 0; k < NT - BS; ++k) fb[k] = *(const f16x8 *)(base + TM * 1024 + n_of(BS + k) * 1024);
+        for (int k = 0; k < NT - BS; ++k) fb[k] = *(const f16x8 *)(base + AOFF + n_of(BS + k) * 1024);
     };
 
     f32x4 acc[MT][NT];
@@ -1710,7 +1716,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
         if (!tail && j2 != 0) {
             constexpr int NM = MT * NT;                       // MFMAs of the stage
             constexpr int NR = (MT - AS) + (NT - BS);         // LDS reads
-            constexpr int NW = AS + BS;                       // LDS writes
+            constexpr int NW = (ASH ? AS : 0) + BS;           // LDS writes
             constexpr int NV = 3;                             // VALU per MFMA slot
 #pragma unroll
             for (int i = 0; i < NM; ++i) {
@@ -1752,14 +1758,18 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     }
 }
 
-// Tiles (rows x columns): 256 x 128 and 128 x 128 on 8 waves, 64 x 64 on 4.
-#define JV_GEMM(NAME, D, TM, TN, WM, WN, ROWS, COLS)                                          \
-    extern "C" __global__ __launch_bounds__(64 * WM * WN) void jv_gemm_##NAME##_##ROWS##x##COLS(GemmParams p) { \
+// Tiles (rows x columns): 256 x 128 and 128 x 128 on 8 waves, 64 x 64 on 4. Q6_K and Q8_0 also
+// have 256 x 128 on 4 waves of 64 x 128 each (activation fragments in registers only, half the
+// LDS traffic), which is faster for them; for Q4_K the 8-wave tile is.
+#define JV_GEMM(NAME, D, TM, TN, WM, WN, ROWS, COLS, SUF)                                     \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN) void jv_gemm_##NAME##_##ROWS##x##COLS##SUF(GemmParams p) { \
         gemm_body<D, TM, TN, WM, WN>(p);                                                      \
     }
 #define JV_GEMM_TILES(NAME, D)                                                                \
-    JV_GEMM(NAME, D, 16, 8, 4, 2, 256, 128) JV_GEMM(NAME, D, 8, 8, 4, 2, 128, 128)          \
-    JV_GEMM(NAME, D, 4, 4, 2, 2, 64, 64)
+    JV_GEMM(NAME, D, 16, 8, 4, 2, 256, 128, ) JV_GEMM(NAME, D, 8, 8, 4, 2, 128, 128, )      \
+    JV_GEMM(NAME, D, 4, 4, 2, 2, 64, 64, )
+JV_GEMM(q6k, DF<FQ6K>, 16, 8, 4, 1, 256, 128, w4)
+JV_GEMM(q8_0, DF<FQ8_0>, 16, 8, 4, 1, 256, 128, w4)
 JV_GEMM_TILES(q4k, DQ4K)
 JV_GEMM_TILES(q6k, DF<FQ6K>)
 JV_GEMM_TILES(q8_0, DF<FQ8_0>)

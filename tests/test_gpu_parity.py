@@ -265,6 +265,24 @@ def test_small_row_products_of_long_rows(gpu, name, type_id, k):
         assert np.array_equal(rows[m], rows[16][:m]), m
 
 
+@pytest.mark.parametrize("name,type_id", [("q6k", jq.Q6K), ("q8_0", jq.Q8_0)])
+def test_four_wave_256x128_tile_equals_the_eight_wave_tile(gpu, monkeypatch, name, type_id):
+    """Q6_K and Q8_0 256 x 128 products run on 4 waves of 64 x 128 by default; the 8-wave tile
+    (JV_GEMM_W4=0) must give the same bits, and both match the f64 oracle."""
+    n, k, m = 384, 1024, 300
+    w, raw = make_matrix(gpu, type_id, n, k, seed=23)
+    x, xv = activations("bf16", synth.normal_rows(29, m, k))
+    want = oracle_product(type_id, raw, n, k, xv)
+    outs = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("JV_GEMM_W4", flag)
+        out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matmul_plan(gpu, x, m, w, out, None, jq.Plan(256, 128, 1))
+        outs.append(out.cpu().numpy())
+        assert err(outs[-1], want) <= TOL, flag
+    assert np.array_equal(outs[0], outs[1])
+
+
 def test_reference_dense_plan_recipe(gpu):
     """every_tunable_dense_plan_matches_reference_and_tiles_are_row_invariant
     (gpu/tests.rs:427-480): Q8_0 N=256 K=512, FP16 rows, every reference plan."""
