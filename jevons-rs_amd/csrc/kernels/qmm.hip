@@ -200,12 +200,17 @@ struct FQ6K {
         const int32_t sc = (int32_t)(int8_t)((sw[grp >> 2] >> (8 * (grp & 3))) & 0xffu);
         const float scale = p.d * (float)sc;  // exact: 11 x 8 significant bits
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int pos = ((e & 1) << 1) | ((e >> 1) & 1);  // stored byte of element e & 3
-            const uint32_t ql = w[qi + (e >> 2)] >> (8 * pos + nib);
-            const uint32_t qh = w[hi + (e >> 2)] >> (8 * pos + 2 * i);
-            const int32_t q = (int32_t)((ql & 15u) | ((qh & 3u) << 4)) - 32;
-            v[e] = scale * (float)q;  // (d * sc) * q, as quant.rs evaluates it
+        for (int h = 0; h < 2; ++h) {
+            // the four 6-bit values q of one word, a byte each (q - 32 is quant.rs's value)
+            uint32_t q6 = ((w[qi + h] >> nib) & 0x0f0f0f0fu) | (((w[hi + h] >> (2 * i)) & 0x03030303u) << 4);
+            asm("" : "+v"(q6));  // one v_cvt_f32_ubyteN per byte
+#pragma unroll
+            for (int e = 4 * h; e < 4 * h + 4; ++e) {
+                const int pos = ((e & 1) << 1) | ((e >> 1) & 1);  // stored byte of element e & 3
+                // (d * sc) * (q - 32) as quant.rs evaluates it (the subtraction is exact; a
+                // fused form would turn quant.rs's -0 for q = 32 and a negative scale into +0)
+                v[e] = scale * ((float)((q6 >> (8 * pos)) & 0xffu) - 32.f);
+            }
         }
     }
 };
@@ -238,11 +243,12 @@ struct FQ8_0 {
     __device__ static int kidx(int s, int g) { return 32 * s + 8 * g; }
     __device__ static void frag_f32(const Raw &r, const Prep &p, int s, int, float v[8]) {
         const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        const float d = p.d[s];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int pos = ((e & 1) << 1) | ((e >> 1) & 1);  // stored byte of element e & 3
-            const int32_t q = (int32_t)((w[2 * s + (e >> 2)] >> (8 * pos)) & 0xffu) - 128;
-            v[e] = p.d[s] * (float)q;
+            // stored byte b = q + 128; b - 128 is exact, and d * q keeps quant.rs's signed zeros
+            v[e] = d * ((float)((w[2 * s + (e >> 2)] >> (8 * pos)) & 0xffu) - 128.f);
         }
     }
 };
@@ -1507,8 +1513,11 @@ __device__ __forceinline__ f16x8 q4k_sub_frag(const Q4KItem &it, int j, float ds
     const int pr = j >> 1;
     const uint32_t w0 = pr == 0 ? it.q0.x : pr == 1 ? it.q0.z : pr == 2 ? it.q1.x : it.q1.z;
     const uint32_t w1 = pr == 0 ? it.q0.y : pr == 1 ? it.q0.w : pr == 2 ? it.q1.y : it.q1.w;
-    const uint32_t n0 = (j & 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
-    const uint32_t n1 = (j & 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
+    uint32_t n0 = (j & 1) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
+    uint32_t n1 = (j & 1) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
+    // Opaque to the compiler, so that each byte converts with one v_cvt_f32_ubyteN instead of a
+    // bit-field extract of the known nibble plus a conversion.
+    asm("" : "+v"(n0), "+v"(n1));
     // stored byte order {0, 2, 1, 3}: byte 1 holds element 2, byte 2 element 1
     const float q[8] = {(float)(uint8_t)n0, (float)(uint8_t)(n0 >> 16), (float)(uint8_t)(n0 >> 8),
                         (float)(uint8_t)(n0 >> 24), (float)(uint8_t)n1, (float)(uint8_t)(n1 >> 16),
