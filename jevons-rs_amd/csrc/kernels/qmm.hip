@@ -572,16 +572,22 @@ __device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int 
     constexpr int XC = XB / LPC;           // chunks held per lane at once
     const int per_row = ncols >> 3;
     const int total = p.M * per_row;  // 8-element chunks; a multiple of 4 (ncols % 32 == 0)
+    // chunk i = row r, 8-column group c8: r = floor((i + 0.5) / per_row) through a float
+    // reciprocal, exact for i < 2^22 (the rounding error stays below the 0.5 / per_row margin)
+    const float rcp = 1.0f / (float)per_row;
     bool issued = false;
     for (int i0 = 0; i0 < total; i0 += XC * 64) {
         uint4 raw[XC][LPC];
+        int rq[XC], cq[XC];
         const int nq = min(XC, (total - i0 + 63) >> 6);  // uniform: batches holding real chunks
 #pragma unroll
         for (int q = 0; q < XC; ++q) {
             if (q >= nq) break;
             const int i = min(i0 + q * 64 + lane, total - 1);
-            const int r = i / per_row;
+            const int r = (int)(((float)i + 0.5f) * rcp);
             const int c8 = i - r * per_row;
+            rq[q] = r;
+            cq[q] = c8;
             const size_t src = (size_t)r * (size_t)p.ldx + (size_t)(c0 + 8 * c8);
 #pragma unroll
             for (int hh = 0; hh < LPC; ++hh) {
@@ -602,8 +608,8 @@ __device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int 
             float part = 0.f;
             int r = 0, c8 = 0;
             if (i < total) {
-                r = i / per_row;
-                c8 = i - r * per_row;
+                r = rq[q];  // i is not clamped here
+                c8 = cq[q];
                 float v[8];
                 if (ACT == 2) {
 #pragma unroll
@@ -651,16 +657,22 @@ __device__ __forceinline__ void stage_group_cols(const QmmParams &p, int c0, int
     constexpr int XC = XB / LPC;           // chunks held per lane at once
     const int per_row = ncols >> 3;
     const int total = p.M * per_row;  // 8-element chunks; a multiple of 4 (ncols % 32 == 0)
+    // chunk i = row r, 8-column group c8: r = floor((i + 0.5) / per_row) through a float
+    // reciprocal, exact for i < 2^22 (the rounding error stays below the 0.5 / per_row margin)
+    const float rcp = 1.0f / (float)per_row;
     bool issued = false;
     for (int i0 = 64 * wave; i0 < total; i0 += XC * 64 * W) {
         uint4 raw[XC][LPC];
+        int rq[XC], cq[XC];
         const int nq = min(XC, (total - i0 + 64 * W - 1) / (64 * W));  // uniform: batches holding real chunks
 #pragma unroll
         for (int q = 0; q < XC; ++q) {
             if (q >= nq) break;
             const int i = min(i0 + q * 64 * W + lane, total - 1);
-            const int r = i / per_row;
+            const int r = (int)(((float)i + 0.5f) * rcp);
             const int c8 = i - r * per_row;
+            rq[q] = r;
+            cq[q] = c8;
             const size_t src = (size_t)r * (size_t)p.ldx + (size_t)(c0 + 8 * c8);
 #pragma unroll
             for (int hh = 0; hh < LPC; ++hh) {
@@ -681,8 +693,8 @@ __device__ __forceinline__ void stage_group_cols(const QmmParams &p, int c0, int
             float part = 0.f;
             int r = 0, c8 = 0;
             if (i < total) {
-                r = i / per_row;
-                c8 = i - r * per_row;
+                r = rq[q];  // i is not clamped here
+                c8 = cq[q];
                 float v[8];
                 if (ACT == 2) {
 #pragma unroll
