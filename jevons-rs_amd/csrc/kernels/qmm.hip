@@ -852,11 +852,13 @@ struct GQ8_0 {
         f32x4 S[2];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
+            // bytes {0, 2} or {1, 3} of a word under the exponent byte 0x64 (byte 1 of magic,
+            // selector 5): FP16 1024 + b with one v_perm_b32 per dword
             uint4 bq;
-            bq.x = (w[2 * b] & 0x00ff00ffu) | magic;
-            bq.y = ((w[2 * b] >> 8) & 0x00ff00ffu) | magic;
-            bq.z = (w[2 * b + 1] & 0x00ff00ffu) | magic;
-            bq.w = ((w[2 * b + 1] >> 8) & 0x00ff00ffu) | magic;
+            bq.x = __builtin_amdgcn_perm(magic, w[2 * b], 0x05020500u);
+            bq.y = __builtin_amdgcn_perm(magic, w[2 * b], 0x05030501u);
+            bq.z = __builtin_amdgcn_perm(magic, w[2 * b + 1], 0x05020500u);
+            bq.w = __builtin_amdgcn_perm(magic, w[2 * b + 1], 0x05030501u);
             S[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xrow + ul * 64 + 32 * b + 8 * g),
                                                           __builtin_bit_cast(f16x8, bq),
                                                           f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
@@ -920,10 +922,14 @@ struct GQ6K {
             const int qi = 2 * (2 * hf + (i & 1)), nib = 4 * (i >> 1);
             u32x4 bq;
 #pragma unroll
-            for (int pr = 0; pr < 4; ++pr) {
-                const uint32_t L = W[qi + (pr >> 1)] >> (8 * (pr & 1) + nib);
-                const uint32_t H = W[8 + 2 * hf + (pr >> 1)] >> (8 * (pr & 1) + 2 * i);
-                bq[pr] = (L & 0x000f000fu) | ((H & 0x00030003u) << 4) | magic;
+            for (int p2 = 0; p2 < 2; ++p2) {
+                // the four 6-bit values of one word, a byte each; v_perm_b32 then puts bytes
+                // {0, 2} or {1, 3} under the exponent byte 0x64: FP16 1024 + q. Selector
+                // bytes 0-3 pick bytes of q6, 5 picks byte 1 of magic (0x64).
+                const uint32_t q6 = ((W[qi + p2] >> nib) & 0x0f0f0f0fu) |
+                                    (((W[8 + 2 * hf + p2] >> (2 * i)) & 0x03030303u) << 4);
+                bq[2 * p2] = __builtin_amdgcn_perm(magic, q6, 0x05020500u);
+                bq[2 * p2 + 1] = __builtin_amdgcn_perm(magic, q6, 0x05030501u);
             }
             const f16x8 bf = __builtin_bit_cast(f16x8, bq);
             const f32x4 S0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xlo + 32 * s), bf,
