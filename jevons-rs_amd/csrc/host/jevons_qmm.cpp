@@ -569,15 +569,16 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         gp.out_type = (int32_t)out_type;
         void *gargs[] = {&gp};
         char name[40];
-        // Q6_K and Q8_0 256 x 128 tiles run on 4 waves of 64 x 128 (same bits as the 8-wave
-        // tile; JV_GEMM_W4=0 selects the 8-wave one).
-        const char *w4env = getenv("JV_GEMM_W4");
-        const bool w4 = plan.bm == 256 && (w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
-                        !(w4env && w4env[0] == '0');
+        // Q4_K, Q6_K and Q8_0 256 x 128 tiles run on 8 waves of 32 x 128 with the activation
+        // fragments in registers (same bits as the 4 x 2-wave tile; JV_GEMM_REG=0 selects that).
+        const char *regenv = getenv("JV_GEMM_REG");
+        const bool reg = plan.bm == 256 &&
+                         (w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
+                         !(regenv && regenv[0] == '0');
         snprintf(name, sizeof name, "jv_gemm_%s_%ux%u%s", fmt_kernel_name(w->fmt), plan.bm, plan.bn,
-                 w4 ? "w4" : "");
-        const unsigned waves = w4 ? 4 : (plan.bm >= 128 ? 8 : 4);
-        const size_t glds = 4 * ((w4 ? 0 : plan.bm) + plan.bn) / 16 * 1024;
+                 reg ? "r" : "");
+        const unsigned waves = plan.bm >= 128 ? 8 : 4;
+        const size_t glds = 4 * ((reg ? 0 : plan.bm) + plan.bn) / 16 * 1024;
         return launch(ctx, name, dim3((unsigned)(w->n / plan.bn), (unsigned)(mtiles * 16 / plan.bm)),
                       dim3(64 * waves), glds, stream, gargs);
     }

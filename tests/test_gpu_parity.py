@@ -265,17 +265,20 @@ def test_small_row_products_of_long_rows(gpu, name, type_id, k):
         assert np.array_equal(rows[m], rows[16][:m]), m
 
 
-@pytest.mark.parametrize("name,type_id", [("q6k", jq.Q6K), ("q8_0", jq.Q8_0)])
-def test_four_wave_256x128_tile_equals_the_eight_wave_tile(gpu, monkeypatch, name, type_id):
-    """Q6_K and Q8_0 256 x 128 products run on 4 waves of 64 x 128 by default; the 8-wave tile
-    (JV_GEMM_W4=0) must give the same bits, and both match the f64 oracle."""
+@pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0)])
+def test_register_activation_256x128_tile_equals_the_lds_tile(gpu, monkeypatch, name, type_id):
+    """Q4_K, Q6_K and Q8_0 256 x 128 products run by default on 8 waves of 32 x 128 that keep
+    their activation fragments in registers, writing three stages ahead with a barrier every
+    second stage; the 4 x 2-wave tile that shares activations through LDS (JV_GEMM_REG=0) must
+    give the same bits, and both match the f64 oracle. K = 1024 is four blocks of 8 stages, so
+    the steady state, the block switches and the tail all run."""
     n, k, m = 384, 1024, 300
     w, raw = make_matrix(gpu, type_id, n, k, seed=23)
     x, xv = activations("bf16", synth.normal_rows(29, m, k))
     want = oracle_product(type_id, raw, n, k, xv)
     outs = []
     for flag in ("1", "0"):
-        monkeypatch.setenv("JV_GEMM_W4", flag)
+        monkeypatch.setenv("JV_GEMM_REG", flag)
         out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
         jq.matmul_plan(gpu, x, m, w, out, None, jq.Plan(256, 128, 1))
         outs.append(out.cpu().numpy())
