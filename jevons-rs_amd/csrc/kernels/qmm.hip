@@ -1791,11 +1791,12 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     }
 }
 
-// Tiles (rows x columns): 256 x 128 and 128 x 128 on 8 waves of 4 x 2, 64 x 64 on 4 waves. Q4_K,
-// Q6_K and Q8_0 also have 256 x 128 on 8 waves of 8 x 1 (suffix r): each wave owns 32 rows x
-// 128 columns and keeps its activation fragments in registers, LDS holds only the weights, and
-// stages are written three ahead with a barrier every second stage (HB). That is the library's
-// 256 x 128 tile for these formats (measured 10-13% faster); the same bits either way.
+// Tiles (rows x columns): 256 x 128 and 128 x 128 on 8 waves of 4 x 2, 64 x 64 on 4 waves of
+// 2 x 2. Q4_K, Q6_K and Q8_0 also have 256 x 128 on 8 waves of 8 x 1 and 64 x 64 on 4 waves of
+// 4 x 1 (suffix r): each wave owns 32 x 128 or 16 x 64 and keeps its activation fragments in
+// registers, LDS holds only the weights, and stages are written three ahead with a barrier
+// every second stage (HB). Those are the library's tiles for these formats (faster in
+// interleaved measurements); the same bits either way.
 #define JV_GEMM(NAME, D, TM, TN, WM, WN, ROWS, COLS, SUF, HB)                                 \
     extern "C" __global__ __launch_bounds__(64 * WM * WN) void jv_gemm_##NAME##_##ROWS##x##COLS##SUF(GemmParams p) { \
         gemm_body<D, TM, TN, WM, WN, HB>(p);                                                  \
@@ -1806,6 +1807,9 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 JV_GEMM(q4k, DQ4K, 16, 8, 8, 1, 256, 128, r, true)
 JV_GEMM(q6k, DF<FQ6K>, 16, 8, 8, 1, 256, 128, r, true)
 JV_GEMM(q8_0, DF<FQ8_0>, 16, 8, 8, 1, 256, 128, r, true)
+JV_GEMM(q4k, DQ4K, 4, 4, 4, 1, 64, 64, r, true)
+JV_GEMM(q6k, DF<FQ6K>, 4, 4, 4, 1, 64, 64, r, true)
+JV_GEMM(q8_0, DF<FQ8_0>, 4, 4, 4, 1, 64, 64, r, true)
 JV_GEMM_TILES(q4k, DQ4K)
 JV_GEMM_TILES(q6k, DF<FQ6K>)
 JV_GEMM_TILES(q8_0, DF<FQ8_0>)

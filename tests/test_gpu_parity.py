@@ -266,24 +266,26 @@ def test_small_row_products_of_long_rows(gpu, name, type_id, k):
 
 
 @pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0)])
-def test_register_activation_256x128_tile_equals_the_lds_tile(gpu, monkeypatch, name, type_id):
-    """Q4_K, Q6_K and Q8_0 256 x 128 products run by default on 8 waves of 32 x 128 that keep
-    their activation fragments in registers, writing three stages ahead with a barrier every
-    second stage; the 4 x 2-wave tile that shares activations through LDS (JV_GEMM_REG=0) must
-    give the same bits, and both match the f64 oracle. K = 1024 is four blocks of 8 stages, so
+def test_register_activation_tiles_equal_the_lds_tiles(gpu, monkeypatch, name, type_id):
+    """Q4_K, Q6_K and Q8_0 256 x 128 and 64 x 64 products run by default on waves (8 x 1, 4 x 1)
+    that keep their activation fragments in registers, writing three stages ahead with a
+    barrier every second stage; the tiles that share activations through LDS (JV_GEMM_REG=0)
+    must give the same bits, and all match the f64 oracle. K = 1024 is four blocks of 8 stages, so
     the steady state, the block switches and the tail all run."""
     n, k, m = 384, 1024, 300
     w, raw = make_matrix(gpu, type_id, n, k, seed=23)
     x, xv = activations("bf16", synth.normal_rows(29, m, k))
     want = oracle_product(type_id, raw, n, k, xv)
     outs = []
-    for flag in ("1", "0"):
-        monkeypatch.setenv("JV_GEMM_REG", flag)
-        out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
-        jq.matmul_plan(gpu, x, m, w, out, None, jq.Plan(256, 128, 1))
-        outs.append(out.cpu().numpy())
-        assert err(outs[-1], want) <= TOL, flag
-    assert np.array_equal(outs[0], outs[1])
+    for plan in (jq.Plan(256, 128, 1), jq.Plan(64, 64, 1)):
+        for flag in ("1", "0"):
+            monkeypatch.setenv("JV_GEMM_REG", flag)
+            out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+            jq.matmul_plan(gpu, x, m, w, out, None, plan)
+            outs.append(out.cpu().numpy())
+            assert err(outs[-1], want) <= TOL, (plan, flag)
+    for o in outs[1:]:
+        assert np.array_equal(outs[0], o)
 
 
 def test_reference_dense_plan_recipe(gpu):
