@@ -569,9 +569,9 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         gp.out_type = (int32_t)out_type;
         void *gargs[] = {&gp};
         char name[40];
-        // Q4_K, Q6_K and Q8_0 256 x 128 and 64 x 64 tiles run on waves of 32 x 128 (8) and
-        // 16 x 64 (4) that keep their activation fragments in registers (same bits as the
-        // tiles that share them through LDS; JV_GEMM_REG=0 selects those).
+        // Q4_K, Q6_K and Q8_0 256 x 128 and 64 x 64 tiles run on waves that keep their
+        // activation fragments in registers (same bits as the tiles that share them through
+        // LDS; JV_GEMM_REG=0 selects those).
         const char *regenv = getenv("JV_GEMM_REG");
         const bool reg = (plan.bm == 256 || plan.bm == 64) &&
                          (w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&

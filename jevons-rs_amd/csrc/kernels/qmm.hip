@@ -1592,10 +1592,12 @@ struct DF {  // any format with the F* interface of the small-tile kernel
 //
 // Each output element is the same MFMA chain over K as in the other tiled kernels (32-k steps
 // in order, lane group g holding k 32s + 8g .. +8), so the result is bitwise identical to theirs.
-template <class D, int TM, int TN, int WM, int WN, bool HB = false>
+template <class D, int TM, int TN, int WM, int WN, bool HB = false, bool APRIV = false>
 __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     constexpr int W = WM * WN, MT = TM / WM, NT = TN / WN;
-    constexpr int AS = MT / WN;  // activation fragments a wave stages per stage (own m slots)
+    // activation fragments a wave loads per stage (own m slots): a share of its MT, or with
+    // APRIV all of them (waves of one row of the wave grid load the same ones)
+    constexpr int AS = APRIV ? MT : MT / WN;
     constexpr int BS = NT / WM;  // weight fragments a wave decodes per stage (own n slots)
     constexpr int UPS = 8 / D::SPU;  // K units per 8 stages
     // Activation fragments go through LDS only when several waves share an m-tile (WN > 1);
@@ -1603,7 +1605,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     constexpr bool ASH = AS < MT;
     constexpr int AOFF = ASH ? TM * 1024 : 0;  // weight fragments' offset in a buffer
     constexpr int BUF = AOFF + TN * 1024;
-    static_assert(AS * W == TM && BS * W == TN && AS >= 1 && BS >= 1, "tile split");
+    static_assert((APRIV || AS * W == TM) && BS * W == TN && AS >= 1 && BS >= 1, "tile split");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1619,7 +1621,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     // Local m-tile of slot i: own slots first (the AS this wave stages), then the rest of the
     // wave's MT in order; n-tile of slot k likewise with the BS tiles it decodes.
     auto m_of = [&](int i) __attribute__((always_inline)) {
-        const int own0 = AS * nh;
+        const int own0 = APRIV ? 0 : AS * nh;
         return MT * mq + (i < AS ? own0 + i : ((own0 + i) % MT));
     };
     auto n_of = [&](int k) __attribute__((always_inline)) {
@@ -1792,24 +1794,31 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 }
 
 // Tiles (rows x columns): 256 x 128 and 128 x 128 on 8 waves of 4 x 2, 64 x 64 on 4 waves of
-// 2 x 2. Q4_K, Q6_K and Q8_0 also have 256 x 128 on 8 waves of 8 x 1 and 64 x 64 on 4 waves of
-// 4 x 1 (suffix r): each wave owns 32 x 128 or 16 x 64 and keeps its activation fragments in
-// registers, LDS holds only the weights, and stages are written three ahead with a barrier
-// every second stage (HB). Those are the library's tiles for these formats (faster in
-// interleaved measurements); the same bits either way.
+// 2 x 2, activation fragments shared through LDS. Q4_K, Q6_K and Q8_0 also have 256 x 128 and
+// 64 x 64 tiles (suffix r) whose waves keep their activation fragments in registers, so LDS
+// holds only the weights, writing stages three ahead with a barrier every second stage (HB):
+// Q4_K and Q6_K 256 x 128 on 8 waves of 8 x 1 (32 x 128 each); Q8_0 256 x 128 and every
+// 64 x 64 on the 4 x 2 / 2 x 2 grid with each wave loading all of its m-tiles (APRIV, waves of
+// one grid row load the same fragments) and reading only its share of the weights from LDS.
+// Those are the library's tiles for these formats (the faster arrangement per format and tile
+// in interleaved measurements); the same bits either way.
 #define JV_GEMM(NAME, D, TM, TN, WM, WN, ROWS, COLS, SUF, HB)                                 \
     extern "C" __global__ __launch_bounds__(64 * WM * WN) void jv_gemm_##NAME##_##ROWS##x##COLS##SUF(GemmParams p) { \
         gemm_body<D, TM, TN, WM, WN, HB>(p);                                                  \
+    }
+#define JV_GEMMP(NAME, D, TM, TN, WM, WN, ROWS, COLS, SUF)                                    \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN) void jv_gemm_##NAME##_##ROWS##x##COLS##SUF(GemmParams p) { \
+        gemm_body<D, TM, TN, WM, WN, true, true>(p);                                          \
     }
 #define JV_GEMM_TILES(NAME, D)                                                                \
     JV_GEMM(NAME, D, 16, 8, 4, 2, 256, 128, , false) JV_GEMM(NAME, D, 8, 8, 4, 2, 128, 128, , false) \
     JV_GEMM(NAME, D, 4, 4, 2, 2, 64, 64, , false)
 JV_GEMM(q4k, DQ4K, 16, 8, 8, 1, 256, 128, r, true)
 JV_GEMM(q6k, DF<FQ6K>, 16, 8, 8, 1, 256, 128, r, true)
-JV_GEMM(q8_0, DF<FQ8_0>, 16, 8, 8, 1, 256, 128, r, true)
-JV_GEMM(q4k, DQ4K, 4, 4, 4, 1, 64, 64, r, true)
-JV_GEMM(q6k, DF<FQ6K>, 4, 4, 4, 1, 64, 64, r, true)
-JV_GEMM(q8_0, DF<FQ8_0>, 4, 4, 4, 1, 64, 64, r, true)
+JV_GEMMP(q8_0, DF<FQ8_0>, 16, 8, 4, 2, 256, 128, r)
+JV_GEMMP(q4k, DQ4K, 4, 4, 2, 2, 64, 64, r)
+JV_GEMMP(q6k, DF<FQ6K>, 4, 4, 2, 2, 64, 64, r)
+JV_GEMMP(q8_0, DF<FQ8_0>, 4, 4, 2, 2, 64, 64, r)
 JV_GEMM_TILES(q4k, DQ4K)
 JV_GEMM_TILES(q6k, DF<FQ6K>)
 JV_GEMM_TILES(q8_0, DF<FQ8_0>)
