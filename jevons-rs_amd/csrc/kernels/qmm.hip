@@ -1481,27 +1481,13 @@ extern "C" __global__ __launch_bounds__(256) void jv_pack_x(PackXParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Q4_K tiled product, 256 x 128 output tile per workgroup of 8 waves (two per SIMD).
-//
-// Wave w = 2 mq + nh computes a 64 x 64 block of the tile: activation m-tiles 4 mq .. 4 mq + 3
-// and weight n-tiles 4 nh .. 4 nh + 3 (16 rows each), 4 x 4 MFMA 16x16x32 accumulators. K
-// advances in stages of 32 (one Q4_K sub-block), in four LDS buffers of 24 KB:
-//   A: the workgroup's 16 activation fragments of the stage (1 KB each, lane order), copied
-//      from jv_pack_x's output. Wave w copies m-tiles 4 mq + 2 nh, +1 (two of its own four);
-//   B: the 8 weight fragments, decoded from Q4_K exactly as quant.rs does (FP32 decode, one RNE
-//      rounding to FP16; gemm.rs:131-284's tile format). Wave w decodes n-tile 4 nh + mq (one
-//      of its own four), so every weight is decoded once per workgroup.
-// A wave takes the two activation and one weight fragment it wrote from its registers and
-// reads the other five from LDS; the reads for stage t + 1 are issued while stage t's MFMAs
-// run, and stage t + 2 is written meanwhile. Register slots are ordered own-first, so which
-// fragment is whose is fixed at compile time.
-//
-// Each output element is the same MFMA chain over K as in the other tiled kernels (32-k steps
-// in order, lane group g holding k 32s + 8g .. +8), so the result is bitwise identical to theirs.
+// Pipelined tiled products (gemm_body below): weight fragments decoded once per workgroup into
+// LDS, activation fragments from jv_pack_x's output, K in 32-k stages. Each output element is
+// the same MFMA chain over K as in the other tiled kernels (32-k steps in order, lane group g
+// holding k 32s + 8g .. +8), so the result is bitwise identical to theirs.
 // ---------------------------------------------------------------------------------------------
 namespace {
 
-constexpr int kGemmBufBytes = 24 * 1024;  // A 16 KB + B 8 KB
 
 // All 8 (d s_j, dmin m_j) of row r of a block, from the lane's head dword (see q4k_item_load):
 // lane group g decodes sub-blocks 2g, 2g + 1, and permlane swaps share them.
