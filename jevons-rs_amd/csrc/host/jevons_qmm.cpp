@@ -569,11 +569,11 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         gp.out_type = (int32_t)out_type;
         void *gargs[] = {&gp};
         char name[40];
-        // Q4_K, Q6_K and Q8_0 256 x 128 and 64 x 64 tiles run on waves that keep their
-        // activation fragments in registers (same bits as the tiles that share them through
-        // LDS; JV_GEMM_REG=0 selects those).
+        // Q4_K, Q6_K and Q8_0 tiles run on waves that keep their activation fragments in
+        // registers (same bits as the tiles that share them through LDS; JV_GEMM_REG=0 selects
+        // those).
         const char *regenv = getenv("JV_GEMM_REG");
-        const bool reg = (plan.bm == 256 || plan.bm == 64) &&
+        const bool reg = (plan.bm == 256 || plan.bm == 128 || plan.bm == 64) &&
                          (w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
                          !(regenv && regenv[0] == '0');
         snprintf(name, sizeof name, "jv_gemm_%s_%ux%u%s", fmt_kernel_name(w->fmt), plan.bm, plan.bn,
@@ -848,8 +848,13 @@ jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
     // of a narrow matrix outside prefill keep the generic tiles, whose split-K fills the device.
     const size_t tiles64 = (cols / 64) * ((m + 63) / 64);
     if (w->k % 256 == 0 && (m >= 48 || row_invariant || tiles64 >= cus)) {
-        if (cols % 128 == 0 && m >= 128 && ((m + 255) / 256) * (cols / 128) * 16 >= cus * 15)
+        // 256 x 128 from 192 rows (at most a quarter of its rows padding), 128 x 128 above 64
+        // rows, each only while its workgroups still fill the device (gate_up at m = 128:
+        // 55 us on 128 x 128 against 69 us on 256 x 128 and 60 us on 64 x 64)
+        if (cols % 128 == 0 && m >= 192 && ((m + 255) / 256) * (cols / 128) * 16 >= cus * 15)
             return jv_plan{256, 128, 1};
+        if (cols % 128 == 0 && m > 64 && ((m + 127) / 128) * (cols / 128) * 16 >= cus * 15)
+            return jv_plan{128, 128, 1};
         if (cols % 64 == 0) return jv_plan{64, 64, 1};
     }
     const uint32_t bm = m <= 32 ? 32 : (m <= 64 ? 64 : 128);

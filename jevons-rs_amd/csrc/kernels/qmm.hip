@@ -745,7 +745,8 @@ __device__ __forceinline__ void q4k_block_fast(const Q4KItem &cur, const _Float1
     const uint4 hd = q4k_head_gather(cur.hv);
     const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
     // scale bytes: y = q[0..3], z = q[4..7], w = q[8..11] (quant.rs:14-23)
-    const uint32_t s_lo = hd.y & 0x3f3f3f3fu;                                   // s_0..s_3
+    uint32_t s_lo = hd.y & 0x3f3f3f3fu;                                         // s_0..s_3
+    asm("" : "+v"(s_lo));  // opaque: each byte converts with one v_cvt_f32_ubyteN
     const uint32_t s_hi = ((hd.y >> 2) & 0x30303030u) | (hd.w & 0x0f0f0f0fu);    // s_4..s_7
     const uint32_t m_hi = ((hd.z >> 2) & 0x30303030u) | ((hd.w >> 4) & 0x0f0f0f0fu);  // m_4..m_7
     const float sg = (float)((s_lo >> sh) & 0xffu), s4g = (float)((s_hi >> sh) & 0xffu);
@@ -1780,12 +1781,12 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 }
 
 // Tiles (rows x columns): 256 x 128 and 128 x 128 on 8 waves of 4 x 2, 64 x 64 on 4 waves of
-// 2 x 2, activation fragments shared through LDS. Q4_K, Q6_K and Q8_0 also have 256 x 128 and
-// 64 x 64 tiles (suffix r) whose waves keep their activation fragments in registers, so LDS
-// holds only the weights, writing stages three ahead with a barrier every second stage (HB):
-// Q4_K and Q6_K 256 x 128 on 8 waves of 8 x 1 (32 x 128 each); Q8_0 256 x 128 and every
-// 64 x 64 on the 4 x 2 / 2 x 2 grid with each wave loading all of its m-tiles (APRIV, waves of
-// one grid row load the same fragments) and reading only its share of the weights from LDS.
+// 2 x 2, activation fragments shared through LDS. Q4_K, Q6_K and Q8_0 also have all three tiles
+// with suffix r, whose waves keep their activation fragments in registers, so LDS holds only
+// the weights, writing stages three ahead with a barrier every second stage (HB): Q4_K and Q6_K
+// 256 x 128 on 8 waves of 8 x 1 (32 x 128 each); Q8_0 256 x 128 and every 128 x 128 and 64 x 64
+// on the 4 x 2 / 2 x 2 grid with each wave loading all of its m-tiles (APRIV, waves of one grid
+// row load the same fragments) and reading only its share of the weights from LDS.
 // Those are the library's tiles for these formats (the faster arrangement per format and tile
 // in interleaved measurements); the same bits either way.
 #define JV_GEMM(NAME, D, TM, TN, WM, WN, ROWS, COLS, SUF, HB)                                 \
@@ -1805,6 +1806,9 @@ JV_GEMMP(q8_0, DF<FQ8_0>, 16, 8, 4, 2, 256, 128, r)
 JV_GEMMP(q4k, DQ4K, 4, 4, 2, 2, 64, 64, r)
 JV_GEMMP(q6k, DF<FQ6K>, 4, 4, 2, 2, 64, 64, r)
 JV_GEMMP(q8_0, DF<FQ8_0>, 4, 4, 2, 2, 64, 64, r)
+JV_GEMMP(q4k, DQ4K, 8, 8, 4, 2, 128, 128, r)
+JV_GEMMP(q6k, DF<FQ6K>, 8, 8, 4, 2, 128, 128, r)
+JV_GEMMP(q8_0, DF<FQ8_0>, 8, 8, 4, 2, 128, 128, r)
 JV_GEMM_TILES(q4k, DQ4K)
 JV_GEMM_TILES(q6k, DF<FQ6K>)
 JV_GEMM_TILES(q8_0, DF<FQ8_0>)

@@ -267,7 +267,7 @@ def test_small_row_products_of_long_rows(gpu, name, type_id, k):
 
 @pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0)])
 def test_register_activation_tiles_equal_the_lds_tiles(gpu, monkeypatch, name, type_id):
-    """Q4_K, Q6_K and Q8_0 256 x 128 and 64 x 64 products run by default on waves (8 x 1, 4 x 1)
+    """Q4_K, Q6_K and Q8_0 256 x 128, 128 x 128 and 64 x 64 products run by default on waves
     that keep their activation fragments in registers, writing three stages ahead with a
     barrier every second stage; the tiles that share activations through LDS (JV_GEMM_REG=0)
     must give the same bits, and all match the f64 oracle. K = 1024 is four blocks of 8 stages, so
@@ -277,7 +277,7 @@ def test_register_activation_tiles_equal_the_lds_tiles(gpu, monkeypatch, name, t
     x, xv = activations("bf16", synth.normal_rows(29, m, k))
     want = oracle_product(type_id, raw, n, k, xv)
     outs = []
-    for plan in (jq.Plan(256, 128, 1), jq.Plan(64, 64, 1)):
+    for plan in (jq.Plan(256, 128, 1), jq.Plan(128, 128, 1), jq.Plan(64, 64, 1)):
         for flag in ("1", "0"):
             monkeypatch.setenv("JV_GEMM_REG", flag)
             out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
@@ -702,6 +702,13 @@ def test_plan_rules_follow_the_reference(gpu):
     assert not jq.Plan(128, 128, 0).valid_for(w, 4)
     # the library's own plan: small-row kernel only when rows may differ from the tiles' bits
     assert jq.Plan.auto(w, 4, row_invariant=False).bm == 0
+    # pipelined tiles by rows on a wide matrix (30720 columns, 240 tile columns of 128): 256 x 128
+    # from 192 rows, 128 x 128 above 64 rows, 64 x 64 below, while the workgroups fill the device
+    if gpu.info.compute_units == 256:
+        wide = jq.QMatrix.upload(gpu, jq.Q4K, 30720, 256, 1, synth.weights(jq.Q4K, 1, 30720, 256))
+        assert jq.Plan.auto(wide, 256, row_invariant=True) == jq.Plan(256, 128, 1)
+        assert jq.Plan.auto(wide, 128, row_invariant=True) == jq.Plan(128, 128, 1)
+        assert jq.Plan.auto(wide, 64, row_invariant=True) == jq.Plan(64, 64, 1)
     for m in (1, 4, 16, 70):
         p = jq.Plan.auto(w, m, row_invariant=True)
         assert p.bm > 0 and p.splits == 1 and p.valid_for(w, m), (m, p)
