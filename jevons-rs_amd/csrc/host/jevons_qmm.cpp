@@ -465,30 +465,33 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         const int U = (int)(w->k / ku);
         const int T = (int)(w->n / 16);
         const int umax = (U + waves - 1) / waves;
-        const bool persist = T >= 8 * cus;
-        const int tw = persist || q6 || m <= 2 ? 1 : 2;
+        const int tw = q6 || m <= 2 ? 1 : 2;  // tiles per workgroup of the per-tile kernels
         // per wave: FP16 activations [m][ku umax + 8], sums [m][ku umax / xg] and, for Q6_K, a
         // zero row [ku umax + 8]. The per-tile kernels reuse it for the wave's tile partials
-        // (tw KB); the persistent ones add two chunks of 2 tiles x waves partials. The kernels
-        // compute the same sizes.
+        // (tw KB); the persistent ones add two chunks of 2 tiles x waves partials; the split-K
+        // ones share one such region per workgroup. The kernels compute the same sizes.
         const size_t row = ((size_t)umax * ku + 8) * 2;
         const size_t stage = ((size_t)m * row + (size_t)m * umax * (ku / xg) * 4 + (q6 ? row : 0) + 15) &
                              ~(size_t)15;
-        const size_t lds = persist ? stage * waves + 2 * 2 * (size_t)waves * 1024
-                                   : std::max(stage, (size_t)tw * 1024) * waves;
+        const size_t lmax = ctx->info.lds_bytes;
+        const size_t lds_persist = stage * waves + 2 * 2 * (size_t)waves * 1024;
+        const size_t lds_tile = std::max(stage, (size_t)tw * 1024) * waves;
+        const bool wide = T >= 8 * cus;
         // Split-K workgroups (with a scratch buffer): `waves` tiles x one of `waves` K slices
         // each, the slice staged once per workgroup (`stage` bytes of LDS). Their reduction
         // through device memory costs a few microseconds at the end, so they serve the products
-        // whose per-tile staging is the larger cost: Q4_K and Q6_K above 8 rows, and any K too
-        // long for the per-tile kernels' LDS.
-        // JV_QMV_SPLIT=0 or 1 overrides the choice where both kernels apply (tests, tuning).
+        // whose per-workgroup staging is the larger cost: Q4_K and Q6_K above 8 rows, wide
+        // matrices whose persistent kernel does not fit in LDS, and any K too long for the
+        // per-tile kernels' LDS. Every choice below computes the same sums, so a row's bits do
+        // not depend on m or on the kernel taken.
+        // JV_QMV_SPLIT=0 or 1 overrides the choice where several kernels apply (tests, tuning).
         const char *force = getenv("JV_QMV_SPLIT");
-        const bool split_ok = scratch && !persist && U >= waves && (size_t)T <= kCounterTiles &&
-                              stage <= ctx->info.lds_bytes;
-        const bool split = split_ok && (lds > ctx->info.lds_bytes ||
-                                        (force && (force[0] == '0' || force[0] == '1')
-                                             ? force[0] == '1'
-                                             : !q8 && m > 8));
+        const bool fsplit = force && force[0] == '1', fnosplit = force && force[0] == '0';
+        const bool split_ok = scratch && U >= waves && (size_t)T <= kCounterTiles && stage <= lmax;
+        const bool persist = !(split_ok && fsplit) && wide && lds_persist <= lmax;
+        const bool split = !persist && split_ok &&
+                           (fsplit || lds_tile > lmax || (!fnosplit && (wide || (!q8 && m > 8))));
+        const size_t lds = persist ? lds_persist : lds_tile;
         if (lds <= ctx->info.lds_bytes || split) {
             QmmParams p{};
             p.x = x;

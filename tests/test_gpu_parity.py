@@ -288,6 +288,34 @@ def test_register_activation_tiles_equal_the_lds_tiles(gpu, monkeypatch, name, t
         assert np.array_equal(outs[0], o)
 
 
+def test_wide_matrix_rows_do_not_depend_on_m_when_the_persistent_kernel_does_not_fit(gpu):
+    """A wide Q6_K matrix (8 tiles of 16 rows per compute unit) at K = 3840: the persistent
+    small-row kernel's LDS fits up to m = 8 but not at m = 16, where the library takes the
+    split-K workgroups (with a scratch buffer) or the per-tile kernels (jv_matvec). Every row
+    must have the same bits for every m and kernel, and match the f64 oracle (first 256 rows)."""
+    cus = gpu.info.compute_units
+    n, k = 16 * 8 * cus, 3840
+    raw = synth.weights(jq.Q6K, 31, n, k)
+    w = jq.QMatrix.upload(gpu, jq.Q6K, n, k, 1, raw)
+    x_all = synth.normal_rows(37, 16, k)
+    scratch = jq.SplitScratch(gpu)
+    rows = {}
+    for m in (1, 8, 16):
+        x, xv = activations("bf16", x_all[:m])
+        say("q6k wide", n, k, "m", m)
+        out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matmul(gpu, x, m, w, out, scratch)
+        rows[m] = out.cpu().numpy()
+        head = raw[:256 * 210 * k // 256].copy()
+        e = err(rows[m][:, :256], oracle_product(jq.Q6K, head, 256, k, xv))
+        assert e <= TOL, f"m={m}: normalized error {e:.2e}"
+    tile = torch.full((16, n), float("nan"), dtype=torch.float32, device="cuda")
+    jq.matvec(gpu, activations("bf16", x_all[:16])[0], 16, w, tile)
+    assert np.array_equal(tile.cpu().numpy(), rows[16])
+    assert np.array_equal(rows[1], rows[16][:1])
+    assert np.array_equal(rows[8], rows[16][:8])
+
+
 def test_reference_dense_plan_recipe(gpu):
     """every_tunable_dense_plan_matches_reference_and_tiles_are_row_invariant
     (gpu/tests.rs:427-480): Q8_0 N=256 K=512, FP16 rows, every reference plan."""
