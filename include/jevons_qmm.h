@@ -81,7 +81,11 @@ typedef struct {
 jv_status jv_type_block(uint32_t ggml_type, uint32_t *elems, uint32_t *bytes);
 
 /* Opens HIP device `device` and loads the gfx950 code object (Gpu::new, lib.rs:181-197).
- * The code object is looked up in $JV_CODE_OBJECT, else next to this library. */
+ * The code object is looked up in $JV_CODE_OBJECT, else next to this library. Like the
+ * reference's Gpu (one queue, not Sync), a context serves one host thread at a time, and its
+ * products run in the order they are queued: the context's own staging buffers (packed
+ * activations; split-K counters and partials of jv_matvec) are reused by every product, so
+ * products of one context must not run concurrently on different streams. */
 jv_status jv_open(int device, jv_ctx **out);
 void jv_close(jv_ctx *ctx);
 jv_status jv_device_info_get(jv_ctx *ctx, jv_device_info *info);

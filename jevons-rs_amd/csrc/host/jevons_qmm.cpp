@@ -139,8 +139,9 @@ struct jv_ctx {
     hipModule_t module = nullptr;
     std::unordered_map<std::string, hipFunction_t> fns;
     jv_device_info info{};
-    void *pack = nullptr;  // packed activation fragments of the 256-row Q4_K product (grows)
+    void *pack = nullptr;  // packed activation fragments of the pipelined tiles (grows)
     size_t pack_bytes = 0;
+    jv_scratch *own = nullptr;  // split-K small-row scratch of products given none (grows)
 };
 
 struct jv_qmatrix {
@@ -487,6 +488,15 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         // JV_QMV_SPLIT=0 or 1 overrides the choice where several kernels apply (tests, tuning).
         const char *force = getenv("JV_QMV_SPLIT");
         const bool fsplit = force && force[0] == '1', fnosplit = force && force[0] == '0';
+        // A product given no scratch buffer (jv_matvec) whose only fitting small-row kernel is
+        // split-K uses the context's own, so that its rows keep the bits of every other m.
+        if (!scratch && lds_tile > lmax && !(wide && lds_persist <= lmax) && stage <= lmax) {
+            if (!ctx->own) {
+                ctx->own = new jv_scratch();
+                ctx->own->ctx = ctx;
+            }
+            scratch = ctx->own;
+        }
         const bool split_ok = scratch && U >= waves && (size_t)T <= kCounterTiles && stage <= lmax;
         const bool persist = !(split_ok && fsplit) && wide && lds_persist <= lmax;
         const bool split = !persist && split_ok &&
@@ -668,6 +678,7 @@ void jv_close(jv_ctx *ctx) {
     if (!ctx) return;
     hipSetDevice(ctx->device);
     if (ctx->pack) hipFree(ctx->pack);
+    jv_scratch_free(ctx->own);
     if (ctx->module) hipModuleUnload(ctx->module);
     delete ctx;
 }

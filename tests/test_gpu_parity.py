@@ -245,8 +245,9 @@ def test_split_k_small_row_products_equal_the_per_tile_kernels(gpu, monkeypatch,
 def test_small_row_products_of_long_rows(gpu, name, type_id, k):
     """K too long for the per-tile kernels' per-wave staging at larger m (the down projection,
     K = 15360): the library takes the split-K workgroups, which stage one K slice per
-    workgroup. Outputs against the f64 oracle; rows independent of m across the switch from
-    per-tile (small m) to split-K kernels."""
+    workgroup, with the caller's scratch buffer or (jv_matvec) the context's own. Outputs
+    against the f64 oracle; rows independent of m across the switch from per-tile (small m)
+    to split-K kernels."""
     n = 576
     w, raw = make_matrix(gpu, type_id, n, k, seed=17)
     scratch = jq.SplitScratch(gpu)
@@ -263,6 +264,12 @@ def test_small_row_products_of_long_rows(gpu, name, type_id, k):
         rows[m] = got
     for m in (1, 4, 8):
         assert np.array_equal(rows[m], rows[16][:m]), m
+    # jv_matvec (no scratch buffer) takes the context's own split-K scratch: the same bits
+    for m in (8, 16):
+        x, _ = activations("bf16", x_all[:m])
+        out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matvec(gpu, x, m, w, out)
+        assert np.array_equal(out.cpu().numpy(), rows[m]), m
 
 
 @pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0)])
