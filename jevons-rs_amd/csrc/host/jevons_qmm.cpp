@@ -449,11 +449,11 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
 
     // Products use expert 0's rows of an expert stack (the first n rows), as the reference's
     // ungrouped kernels do (wrow = expert * n + col with expert 0, gemm.rs:463-464).
-    // Small-row Q4_K, Q6_K and Q8_0 kernels. Up to 8 tiles (16 rows) per compute unit: one
-    // workgroup per one or two tiles (two from m = 3 on for Q4_K and Q8_0, which halves the
-    // activation staging per weight byte), or split-K workgroups (below). Wider matrices:
-    // persistent workgroups that stage the activations once and stream a range of tiles. All
-    // variants sum each output element the same way, so every output row is the same for any m.
+    // Small-row Q4_K, Q6_K and Q8_0 kernels: one workgroup per tile (m <= 2, up to 8 tiles
+    // per compute unit); persistent workgroups that stage the activations once and stream a
+    // range of tiles (wide matrices, and m > 2); split-K workgroups (below); one workgroup per
+    // one or two tiles where the persistent kernel does not fit. All variants sum each output
+    // element the same way, so every output row is the same for any m.
     if (plan.bm == 0 && (w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
         w->n * w->experts * w->k < (1ull << 32)) {
         const bool q8 = w->fmt == JV_FMT_Q8_0, q6 = w->fmt == JV_FMT_Q6K;
@@ -498,7 +498,13 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
             scratch = ctx->own;
         }
         const bool split_ok = scratch && U >= waves && (size_t)T <= kCounterTiles && stage <= lmax;
-        const bool persist = !(split_ok && fsplit) && wide && lds_persist <= lmax;
+        // Persistent workgroups stage the activations once for several tiles: they serve wide
+        // matrices and, above 2 rows, any matrix (at m = 4-8 on the decode shapes 10-34% faster
+        // than the per-tile kernels, whose staging per tile or tile pair dominates there).
+        // JV_QMV_PERSIST=0 keeps the per-tile kernels above 2 rows (tests).
+        const char *pforce = getenv("JV_QMV_PERSIST");
+        const bool many = m > 2 && !(pforce && pforce[0] == '0');
+        const bool persist = !(split_ok && fsplit) && (wide || many) && lds_persist <= lmax;
         const bool split = !persist && split_ok &&
                            (fsplit || lds_tile > lmax || (!fnosplit && (wide || (!q8 && m > 8))));
         const size_t lds = persist ? lds_persist : lds_tile;

@@ -160,7 +160,7 @@ def test_small_row_product_of_wide_matrices(gpu, name, type_id):
     """Matrices with at least 8 tiles of 16 rows per compute unit take the persistent small-row
     kernels (activations staged once per workgroup, a range of tiles each): every output against
     the f64 oracle, every row independent of m, and a row of the wide matrix equal to the same
-    weight row in a narrow matrix (the per-tile kernels)."""
+    weight row in a narrow matrix (per-tile kernels at m = 1, persistent ones at m = 5)."""
     cus = gpu.info.compute_units
     n = 64 * (2 * cus + 1)  # 8 tiles per compute unit and 4 more: not a multiple of the grid
     k = 512
@@ -321,6 +321,27 @@ def test_wide_matrix_rows_do_not_depend_on_m_when_the_persistent_kernel_does_not
     assert np.array_equal(tile.cpu().numpy(), rows[16])
     assert np.array_equal(rows[1], rows[16][:1])
     assert np.array_equal(rows[8], rows[16][:8])
+
+
+@pytest.mark.parametrize("name,type_id,k", [("q4k", jq.Q4K, 3840), ("q6k", jq.Q6K, 3840), ("q8_0", jq.Q8_0, 4096)])
+def test_persistent_and_per_tile_kernels_agree_above_two_rows(gpu, monkeypatch, name, type_id, k):
+    """Above 2 rows the library streams every matrix with the persistent small-row kernels;
+    the per-tile kernels (JV_QMV_PERSIST=0) must give the same bits at every m, and both match
+    the f64 oracle."""
+    n = 576
+    w, raw = make_matrix(gpu, type_id, n, k, seed=41)
+    x_all = synth.normal_rows(43, 8, k)
+    for m in (3, 4, 5, 8):
+        x, xv = activations("bf16", x_all[:m])
+        outs = []
+        for flag in ("1", "0"):
+            monkeypatch.setenv("JV_QMV_PERSIST", flag)
+            out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+            jq.matvec(gpu, x, m, w, out)
+            outs.append(out.cpu().numpy())
+        assert np.array_equal(outs[0], outs[1]), m
+        e = err(outs[0], oracle_product(type_id, raw, n, k, xv))
+        assert e <= TOL, f"m={m}: normalized error {e:.2e}"
 
 
 def test_reference_dense_plan_recipe(gpu):
