@@ -1303,8 +1303,9 @@ __device__ __forceinline__ void qmvs_body(const QmmParams &p) {
 }  // namespace
 
 // One-tile workgroups run four per compute unit (8 waves per SIMD, at most 64 VGPRs); the
-// library takes them for M <= 2 and two-tile workgroups (half the activation staging per weight
-// byte) for larger M. MV = output rows kept per lane group (M = 1, 2, or up to 16).
+// library takes them for M <= 2, and two-tile workgroups (half the activation staging per weight
+// byte) for larger M where the persistent kernel does not fit. MV = output rows kept per lane
+// group (M = 1, 2, or up to 16).
 #define JV_QMV(TW, MV, XB)                                                                   \
     extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(TW == 1 ? 8 : 4))) \
     void jv_qmv_q4k_t##TW##_m##MV(QmmParams p) {                                             \
@@ -1312,8 +1313,6 @@ __device__ __forceinline__ void qmvs_body(const QmmParams &p) {
     }
 JV_QMV(1, 1, 2)
 JV_QMV(1, 2, 4)
-JV_QMV(2, 1, 4)
-JV_QMV(2, 2, 4)
 JV_QMV(2, 4, 8)
 
 // Q6_K: 8 waves, each two blocks of a tile at K = 3840 (all in flight); one tile per workgroup.
@@ -1347,8 +1346,6 @@ JV_QMVP(q8_0, GQ8_0, 16, 4, 8)
     }
 JV_QMV8(1, 1, 2)
 JV_QMV8(1, 2, 4)
-JV_QMV8(2, 1, 4)
-JV_QMV8(2, 2, 4)
 JV_QMV8(2, 4, 8)
 
 // Split-K kernels: W tiles x one K slice per workgroup (activation staging shared by the waves).
