@@ -428,6 +428,84 @@ jv_status launch_tiles(jv_ctx *ctx, const void *x, jv_act act, size_t m, const j
                   stream, rargs);
 }
 
+// Pipelined tile kernels (256 x 128, 128 x 128, 64 x 64; whole K in 256-element blocks):
+// activations -> packed FP16 fragments (per job when grouped), then the product. Every output
+// element is the same MFMA chain as in the generic tile kernel, so the plans give the same bits.
+bool pipelined_plan(const jv_qmatrix *w, jv_plan plan) {
+    return plan.splits == 1 && w->k % 256 == 0 &&
+           ((plan.bm == 256 && plan.bn == 128) || (plan.bm == 128 && plan.bn == 128) ||
+            (plan.bm == 64 && plan.bn == 64));
+}
+
+jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, const jv_qmatrix *w,
+                           void *out, jv_out out_type, jv_plan plan, void *stream,
+                           const GroupArgs *grp) {
+    jv_status st = JV_OK;
+    const int jobs_or_tiles = grp ? (int)grp->max_jobs : (int)((m + plan.bm - 1) / plan.bm);
+    const int mtiles = jobs_or_tiles * (int)(plan.bm / 16);
+    const size_t need = (size_t)mtiles * 16 * w->k * 2;
+    if (ctx->pack_bytes < need) {
+        if (ctx->pack) JV_HIP(hipFree(ctx->pack));
+        ctx->pack = nullptr;
+        ctx->pack_bytes = 0;
+        JV_HIP(hipMalloc(&ctx->pack, need));
+        ctx->pack_bytes = need;
+    }
+    PackXParams pk{};
+    pk.x = x;
+    pk.out = (uint16_t *)ctx->pack;
+    pk.M = (int32_t)m;
+    pk.K = (int32_t)w->k;
+    pk.ldx = (int32_t)w->k;
+    pk.act = (int32_t)act;
+    pk.mtiles = mtiles;
+    if (grp) {
+        pk.ids = grp->ids;
+        pk.offsets = grp->offsets;
+        pk.jobs = grp->jobs;
+        pk.grouped = 1;
+        pk.in_div = (int32_t)grp->in_div;
+        pk.rows_cap = (int32_t)plan.bm;
+    }
+    const int64_t threads = (int64_t)mtiles * (int64_t)(w->k / 256) * 2 * 64;
+    void *pargs[] = {&pk};
+    st = launch(ctx, "jv_pack_x", dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, pargs);
+    if (st != JV_OK) return st;
+    GemmParams gp{};
+    gp.xa = (const uint16_t *)ctx->pack;
+    gp.wq = w->q;
+    gp.wh = w->h;
+    gp.wd = w->d;
+    gp.out = out;
+    gp.M = (int32_t)m;
+    gp.N = (int32_t)(w->n);
+    gp.K = (int32_t)w->k;
+    gp.ldo = (int32_t)(w->n);
+    gp.out_type = (int32_t)out_type;
+    if (grp) {
+        gp.ids = grp->ids;
+        gp.offsets = grp->offsets;
+        gp.jobs = grp->jobs;
+        gp.grouped = 1;
+        gp.rows_cap = (int32_t)plan.bm;
+    }
+    void *gargs[] = {&gp};
+    char name[40];
+    // Q4_K, Q6_K and Q8_0 tiles run on waves that keep their activation fragments in
+    // registers (same bits as the tiles that share them through LDS; JV_GEMM_REG=0 selects
+    // those).
+    const char *regenv = getenv("JV_GEMM_REG");
+    const bool reg = (plan.bm == 256 || plan.bm == 128 || plan.bm == 64) &&
+                     (w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
+                     !(regenv && regenv[0] == '0');
+    snprintf(name, sizeof name, "jv_gemm_%s_%ux%u%s", fmt_kernel_name(w->fmt), plan.bm, plan.bn,
+             reg ? "r" : "");
+    const unsigned waves = plan.bm >= 128 ? 8 : 4;
+    const size_t glds = 4 * ((reg ? 0 : plan.bm) + plan.bn) / 16 * 1024;
+    return launch(ctx, name, dim3((unsigned)(w->n / plan.bn), (unsigned)jobs_or_tiles),
+                  dim3(64 * waves), glds, stream, gargs);
+}
+
 jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
                       const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
                       jv_plan plan, jv_scratch *scratch, void *stream) {
@@ -548,60 +626,7 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
             return launch(ctx, name, dim3((unsigned)((T + tw - 1) / tw)), dim3(64 * waves), lds, stream, args);
         }
     }
-    // Pipelined tile kernels (256 x 128, 128 x 128, 64 x 64; whole K in 256-element blocks):
-    // activations -> packed FP16 fragments, then the product. Every output element is the same
-    // MFMA chain as in the generic tile kernel, so the plans give the same bits.
-    if (plan.splits == 1 && w->k % 256 == 0 &&
-        ((plan.bm == 256 && plan.bn == 128) || (plan.bm == 128 && plan.bn == 128) ||
-         (plan.bm == 64 && plan.bn == 64))) {
-        const int mtiles = (int)((m + plan.bm - 1) / plan.bm) * (int)(plan.bm / 16);
-        const size_t need = (size_t)mtiles * 16 * w->k * 2;
-        if (ctx->pack_bytes < need) {
-            if (ctx->pack) JV_HIP(hipFree(ctx->pack));
-            ctx->pack = nullptr;
-            ctx->pack_bytes = 0;
-            JV_HIP(hipMalloc(&ctx->pack, need));
-            ctx->pack_bytes = need;
-        }
-        PackXParams pk{};
-        pk.x = x;
-        pk.out = (uint16_t *)ctx->pack;
-        pk.M = (int32_t)m;
-        pk.K = (int32_t)w->k;
-        pk.ldx = (int32_t)w->k;
-        pk.act = (int32_t)act;
-        pk.mtiles = mtiles;
-        const int64_t threads = (int64_t)mtiles * (int64_t)(w->k / 256) * 2 * 64;
-        void *pargs[] = {&pk};
-        st = launch(ctx, "jv_pack_x", dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, pargs);
-        if (st != JV_OK) return st;
-        GemmParams gp{};
-        gp.xa = (const uint16_t *)ctx->pack;
-        gp.wq = w->q;
-        gp.wh = w->h;
-        gp.wd = w->d;
-        gp.out = out;
-        gp.M = (int32_t)m;
-        gp.N = (int32_t)(w->n);
-        gp.K = (int32_t)w->k;
-        gp.ldo = (int32_t)(w->n);
-        gp.out_type = (int32_t)out_type;
-        void *gargs[] = {&gp};
-        char name[40];
-        // Q4_K, Q6_K and Q8_0 tiles run on waves that keep their activation fragments in
-        // registers (same bits as the tiles that share them through LDS; JV_GEMM_REG=0 selects
-        // those).
-        const char *regenv = getenv("JV_GEMM_REG");
-        const bool reg = (plan.bm == 256 || plan.bm == 128 || plan.bm == 64) &&
-                         (w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
-                         !(regenv && regenv[0] == '0');
-        snprintf(name, sizeof name, "jv_gemm_%s_%ux%u%s", fmt_kernel_name(w->fmt), plan.bm, plan.bn,
-                 reg ? "r" : "");
-        const unsigned waves = plan.bm >= 128 ? 8 : 4;
-        const size_t glds = 4 * ((reg ? 0 : plan.bm) + plan.bn) / 16 * 1024;
-        return launch(ctx, name, dim3((unsigned)(w->n / plan.bn), (unsigned)(mtiles * 16 / plan.bm)),
-                      dim3(64 * waves), glds, stream, gargs);
-    }
+    if (pipelined_plan(w, plan)) return launch_pipelined(ctx, x, act, m, w, out, out_type, plan, stream, nullptr);
     return launch_tiles(ctx, x, act, m, w, out, out_type, scratch, plan, stream, nullptr);
 }
 
@@ -1011,6 +1036,12 @@ jv_status jv_matmul_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len
         return fail(JV_ERR_INVALID, "splits = %u is out of range", splits);
     if (g->rows == 0 || g->max_jobs == 0) return JV_OK;
     GroupArgs ga{g->ids, g->offsets, g->jobs, g->max_jobs, g->in_div, bm};
+    // 64 x 64 and 128 x 128 jobs on the pipelined tiles (same bits as the generic tiles) while
+    // the per-job packed activations stay within 1 GiB
+    if (bm != 256 && pipelined_plan(w, jv_plan{bm, bn, splits}) &&
+        g->max_jobs * bm * w->k * 2 <= (1ull << 30))
+        return launch_pipelined(ctx, x, act, g->rows, w, out, out_type, jv_plan{bm, bn, splits},
+                                stream, &ga);
     return launch_tiles(ctx, x, act, g->rows, w, out, out_type, scratch, jv_plan{bm, bn, splits},
                         stream, &ga);
 }

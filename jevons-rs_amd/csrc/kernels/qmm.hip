@@ -1430,11 +1430,22 @@ extern "C" __global__ __launch_bounds__(256) void jv_pack_x(PackXParams p) {
     const int64_t q = t >> 6;
     const int half = (int)(q & 1);
     const int64_t mu = q >> 1;
-    const int row = (int)(mu / U) * 16 + (lane & 15);
+    int row = (int)(mu / U) * 16 + (lane & 15);
+    bool live = row < p.M;
+    if (p.grouped) {  // m-tile mu / U is m-tile (mu / U) % per of job (mu / U) / per
+        const int per = p.rows_cap >> 4;
+        const int mtg = (int)(mu / U);
+        const int job = mtg / per;
+        const int r = (mtg - job * per) * 16 + (lane & 15);
+        if (job >= (int)p.jobs[0]) return;  // no product workgroup reads unused job slots
+        const uint32_t e = p.jobs[1 + 2 * job], s0 = p.jobs[2 + 2 * job];
+        live = r < min((int)(p.offsets[e + 1] - s0), p.rows_cap);
+        if (live) row = (int)(p.ids[s0 + r] / (uint32_t)p.in_div);
+    }
     const int col0 = (int)(mu % U) * 256 + half * 128 + (lane >> 4) * 8;
     uint16_t *dst = p.out + ((mu * 8 + 4 * half) * 64 + lane) * 8;
     f16x8 h[4];
-    if (row < p.M) {
+    if (live) {
         const size_t o = (size_t)row * (size_t)p.ldx + (size_t)col0;
         if (p.act == 0) {
             uint4 w[4];
@@ -1599,6 +1610,16 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     const int UK = U8 * UPS;          // K units
     const int mt0 = blockIdx.y * TM;  // first 16-row activation tile
     const int t0 = blockIdx.x * TN;   // first 16-row weight tile
+    // expert-grouped: job blockIdx.y, its expert's weight tiles, rows, first sorted position
+    int wt0 = 0, rows_real = 0, js = 0;
+    if (p.grouped) {
+        const int job = blockIdx.y;
+        if (job >= (int)p.jobs[0]) return;  // workgroup-uniform, before any barrier
+        const uint32_t e = p.jobs[1 + 2 * job];
+        js = (int)p.jobs[2 + 2 * job];
+        rows_real = min((int)(p.offsets[e + 1] - (uint32_t)js), p.rows_cap);
+        wt0 = (int)e * (p.N >> 4);
+    }
     const int stages = 8 * U8;
     const uint32_t lo16 = (uint32_t)lane * 16u;  // this lane's bytes in a 1 KB fragment
 
@@ -1638,7 +1659,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 #pragma unroll
         for (int q = 0; q < UPS; ++q)
 #pragma unroll
-            for (int k = 0; k < BS; ++k) D::load(dst[q][k], p, t0 + n_of(k), min(UPS * b + q, UK - 1), g, r);
+            for (int k = 0; k < BS; ++k) D::load(dst[q][k], p, wt0 + t0 + n_of(k), min(UPS * b + q, UK - 1), g, r);
     };
     typename D::Prep pp[UPS][BS];
     auto block_prep = [&](const typename D::Raw (*it)[BS]) __attribute__((always_inline)) {
@@ -1764,8 +1785,14 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
             const int col = (t0 + n_of(k)) * 16 + r;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int m = (mt0 + m_of(i)) * 16 + 4 * g + e;
-                if (m < p.M) {
+                int m = (mt0 + m_of(i)) * 16 + 4 * g + e;
+                bool live = m < p.M;
+                if (p.grouped) {
+                    const int ml = m_of(i) * 16 + 4 * g + e;  // row within the job
+                    live = ml < rows_real;
+                    if (live) m = (int)p.ids[js + ml];
+                }
+                if (live) {
                     const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
                     if (f32_out)
                         ((float *)p.out)[o] = acc[i][k][e];

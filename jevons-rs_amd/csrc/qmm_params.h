@@ -48,6 +48,10 @@ struct PackXParams {
     uint16_t *out;       // FP16 bits, mtiles * (K / 32) fragments of 512 elements
     int32_t M, K, ldx, act;
     int32_t mtiles;      // 16-row tiles packed (M rounded up to the product's row tile)
+    // Expert-grouped mode: m-tiles [j rows_cap / 16, (j + 1) rows_cap / 16) hold job j's rows,
+    // input rows ids[s] / in_div for sorted positions s of the job (QmmParams' job format).
+    const uint32_t *ids, *offsets, *jobs;
+    int32_t grouped, in_div, rows_cap;
 };
 
 // Tiled product over packed activation fragments (jv_pack_x output).
@@ -58,6 +62,10 @@ struct GemmParams {
     const uint8_t *wd;
     void *out;           // [M][ldo] of `out_type`
     int32_t M, N, K, ldo, out_type;
+    // Expert-grouped mode (grid y = job): the job's rows come packed per job, its weight rows
+    // start at expert * N, and its output rows are ids[start + r] (QmmParams' job format).
+    const uint32_t *ids, *offsets, *jobs;
+    int32_t grouped, rows_cap;
 };
 
 // GGML blocks (device copy of the upload) -> device layout.

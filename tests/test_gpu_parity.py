@@ -528,6 +528,35 @@ def test_grouped_products_of_other_formats(gpu, name, type_id):
         assert e <= (TOL if out_dtype == torch.float32 else 8e-3), (out_dtype, e)
 
 
+@pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0), ("q5_0", jq.Q5_0)])
+def test_grouped_products_on_the_pipelined_tiles(gpu, name, type_id):
+    """Grouped jobs of 64 and 128 rows run on the pipelined tiles (rows gathered per job into
+    packed fragments, the expert's weight rows, scattered output rows). They must give the
+    bits of the generic grouped tiles (32-row jobs) and match the f64 oracle, with experts of
+    several jobs, a partly filled last job and an empty expert; f32 and bf16 outputs."""
+    experts, n, k, top_k, tokens = 8, 256, 512, 2, 150
+    raw = synth.weights(type_id, 51, experts * n, k)
+    w = jq.QMatrix.upload(gpu, type_id, n, k, experts, raw)
+    dense = O.dequantize(type_id, raw).reshape(experts * n, k)
+    x, xv = activations("bf16", synth.normal_rows(52, tokens, k))
+    rng = np.random.default_rng(53)
+    ids = rng.choice([0, 0, 0, 1, 1, 2, 3, 3, 3, 3, 5, 6, 7], tokens * top_k).astype(np.uint32)  # expert 4 empty
+    want = O.grouped_product_f64(xv, dense, ids, top_k, n)
+    g32 = jq.group_routes(gpu, _i32(ids), experts, 32, in_div=top_k)
+    ref = torch.full((ids.size, n), float("nan"), dtype=torch.float32, device="cuda")
+    jq.matmul_grouped(gpu, x, w, g32, ref, 32, 64, 1, None)
+    ref = ref.cpu().numpy()
+    assert err(ref, want) <= TOL
+    for bm, bn in ((64, 64), (128, 128)):
+        g = jq.group_routes(gpu, _i32(ids), experts, bm, in_div=top_k)
+        out = torch.full((ids.size, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matmul_grouped(gpu, x, w, g, out, bm, bn, 1, None)
+        assert np.array_equal(out.cpu().numpy(), ref), (bm, bn)
+        o16 = torch.zeros((ids.size, n), dtype=torch.bfloat16, device="cuda")
+        jq.matmul_grouped(gpu, x, w, g, o16, bm, bn, 1, None)
+        assert err(o16.float().cpu().numpy(), want) <= 8e-3, (bm, bn)
+
+
 # ------------------------------------------------------------------ lm_head argmax
 
 def test_argmax_follows_greedy(gpu):
