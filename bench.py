@@ -186,8 +186,9 @@ def measure_traffic(wbytes):
 def measure_configs(gpu, steps):
     """Kernel durations of the other product configurations, each against its roofline:
     Q8_0 GEMV (M=1, K=N=4096; weights rotated), the six layer GEMMs of one transformer block at
-    M=256 (Q4_K q/k/v/o/gate_up, Q6_K down), and the Q6_K vocabulary projection (K=3840,
-    N=262144, M = 1, 8, 32) with the per-row argmax of its logits."""
+    M=256 (Q4_K q/k/v/o/gate_up, Q6_K down), the Q6_K vocabulary projection (K=3840,
+    N=262144, M = 1, 8, 32) with the per-row argmax of its logits, and an expert-grouped
+    Q4_K product (the routing step's gate/up shape)."""
     import numpy as np
     import torch
 
@@ -268,6 +269,29 @@ def measure_configs(gpu, steps):
     res["q6k_lm_head"] = {"workload": f"Q6_K vocabulary projection K={k} N={n} + per-row argmax, bf16 activations, f32 logits",
                           "weight_bytes": wbytes, "per_m": lm}
     log("q6k lm_head:", res["q6k_lm_head"])
+    # expert-grouped product (MoE gate/up): 128 Q4_K experts [1408, 2816], 512 tokens routed to
+    # 8 experts each (seeded uniform routing), grouped into 64-row jobs on the device
+    experts, n, k, tokens, top_k = 128, 1408, 2816, 512, 8
+    raw = synth.weights(jq.Q4K, 6, experts * n, k)
+    w = jq.QMatrix.upload_device(gpu, jq.Q4K, n, k, experts, torch.from_numpy(raw).cuda())
+    rng = np.random.default_rng(7)
+    route = np.stack([rng.choice(experts, top_k, replace=False) for _ in range(tokens)]).reshape(-1)
+    ids = torch.from_numpy(route.astype(np.int32)).cuda()
+    x = xrows(tokens, k, 8)
+    out = torch.empty((tokens * top_k, n), dtype=torch.float32, device="cuda")
+    g = jq.group_routes(gpu, ids, experts, 64, in_div=top_k)
+    jq.matmul_grouped(gpu, x, w, g, out, 64, 64, 1, scratch)
+    t = kernel_time_ms(lambda r: jq.matmul_grouped(gpu, x, w, g, out, 64, 64, 1, scratch), max(4, steps // 10))
+    flops = 2.0 * tokens * top_k * n * k
+    tf = flops / (t * 1e-3) / 1e12
+    res["moe_grouped"] = {"workload": f"Q4_K expert-grouped product, {experts} experts N={n} K={k}, {tokens} tokens x top-{top_k}, "
+                                      "64-row jobs, bf16 activations, f32 out",
+                          "kernel_us": round(t * 1e3, 2), "weight_bytes": raw.size,
+                          "weight_GBps": round(raw.size / (t * 1e-3) / 1e9, 1),
+                          "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                                       "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}}
+    del w
+    log("moe grouped:", res["moe_grouped"])
     return res
 
 

@@ -1993,40 +1993,81 @@ JV_PICK(f16, FF16)
 // workgroup: sorted[] lists the assignments of expert 0, then 1, ... (each in assignment order),
 // offsets[e] is expert e's first sorted position (offsets[experts] = routed count), jobs[0] the
 // number of bm-row tiles and jobs[1 + 2j], jobs[2 + 2j] tile j's (expert, first position).
-// Ids >= experts are not routed. Thread t handles experts t, t + 256, ...; experts <= 1024.
-extern "C" __global__ __launch_bounds__(256) void jv_group_routes(const uint32_t *ids, uint32_t assignments,
+// Ids >= experts are not routed; experts <= 1024.
+extern "C" __global__ __launch_bounds__(512) void jv_group_routes(const uint32_t *ids, uint32_t assignments,
                                                                   uint32_t experts, uint32_t bm,
                                                                   uint32_t *sorted, uint32_t *offsets,
                                                                   uint32_t *jobs) {
-    __shared__ uint32_t counts[1024], starts[1025], jstarts[1025];
-    for (uint32_t e = threadIdx.x; e < experts; e += 256) {
-        uint32_t c = 0;
-        for (uint32_t a = 0; a < assignments; ++a) c += ids[a] == e;
-        counts[e] = c;
+    // A stable counting sort in one workgroup of NW waves. Wave w owns the contiguous
+    // assignments [a0, a1): it counts them per expert, the counts become per-wave starting
+    // positions (expert start + the counts of earlier waves), and the wave places its
+    // assignments in order, ranking the lanes of one expert within each 64-assignment batch by
+    // ballot. So every expert's positions hold its assignments in increasing order.
+    constexpr int NW = 8;
+    __shared__ uint32_t cnt[NW][1024];
+    __shared__ uint32_t starts[1025], jst[1025];
+    const int tid = (int)threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    for (int i = tid; i < NW * 1024; i += 64 * NW) cnt[i >> 10][i & 1023] = 0;
+    __syncthreads();
+    const uint32_t per = (assignments + NW - 1) / NW;
+    const uint32_t a0 = min((uint32_t)wv * per, assignments), a1 = min(a0 + per, assignments);
+    for (uint32_t c = a0; c < a1; c += 64) {
+        const uint32_t a = c + (uint32_t)lane;
+        if (a < a1) {
+            const uint32_t ex = ids[a];
+            if (ex < experts) atomicAdd(&cnt[wv][ex], 1u);
+        }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    for (uint32_t ex = (uint32_t)tid; ex < experts; ex += 64 * NW) {  // counts -> wave prefixes
+        uint32_t sum = 0;
+        for (int w = 0; w < NW; ++w) {
+            const uint32_t c = cnt[w][ex];
+            cnt[w][ex] = sum;
+            sum += c;
+        }
+        starts[ex] = sum;
+    }
+    __syncthreads();
+    if (tid == 0) {
         uint32_t acc = 0, jacc = 0;
-        for (uint32_t e = 0; e < experts; ++e) {
-            starts[e] = acc;
-            jstarts[e] = jacc;
-            acc += counts[e];
-            jacc += (counts[e] + bm - 1) / bm;
+        for (uint32_t ex = 0; ex < experts; ++ex) {
+            const uint32_t c = starts[ex];
+            starts[ex] = acc;
+            jst[ex] = jacc;
+            acc += c;
+            jacc += (c + bm - 1) / bm;
         }
         starts[experts] = acc;
         offsets[experts] = acc;
         jobs[0] = jacc;
     }
     __syncthreads();
-    for (uint32_t e = threadIdx.x; e < experts; e += 256) {
-        offsets[e] = starts[e];
-        uint32_t next = starts[e];
-        for (uint32_t a = 0; a < assignments; ++a)
-            if (ids[a] == e) sorted[next++] = a;
-        const uint32_t tiles = (counts[e] + bm - 1) / bm;
+    for (uint32_t ex = (uint32_t)tid; ex < experts; ex += 64 * NW) {
+        offsets[ex] = starts[ex];
+        const uint32_t tiles = (starts[ex + 1] - starts[ex] + bm - 1) / bm;
         for (uint32_t t = 0; t < tiles; ++t) {
-            jobs[1 + 2 * (jstarts[e] + t)] = e;
-            jobs[2 + 2 * (jstarts[e] + t)] = starts[e] + t * bm;
+            jobs[1 + 2 * (jst[ex] + t)] = ex;
+            jobs[2 + 2 * (jst[ex] + t)] = starts[ex] + t * bm;
+        }
+    }
+    for (uint32_t c = a0; c < a1; c += 64) {
+        const uint32_t a = c + (uint32_t)lane;
+        const uint32_t ex = a < a1 ? ids[a] : 0xffffffffu;
+        bool todo = ex < experts;
+        for (;;) {
+            const uint64_t active = __ballot(todo);
+            if (active == 0) break;
+            const int first = __ffsll((unsigned long long)active) - 1;
+            const uint32_t ef = (uint32_t)__shfl((int)ex, first);
+            const bool mine = todo && ex == ef;
+            const uint64_t same = __ballot(mine);
+            const uint32_t base = starts[ef] + cnt[wv][ef];
+            if (mine) {
+                sorted[base + (uint32_t)__popcll(same & ((1ull << lane) - 1))] = a;
+                todo = false;
+            }
+            if (lane == first) cnt[wv][ef] = cnt[wv][ef] + (uint32_t)__popcll(same);
         }
     }
 }

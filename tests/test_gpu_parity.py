@@ -458,7 +458,8 @@ def _i32(a: np.ndarray):
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).cuda()
 
 
-@pytest.mark.parametrize("experts,bm,a", [(4, 32, 42), (8, 16, 300), (128, 64, 2048), (3, 128, 5)])
+@pytest.mark.parametrize("experts,bm,a", [(4, 32, 42), (8, 16, 300), (128, 64, 2048), (3, 128, 5),
+                                          (1024, 16, 20000), (128, 64, 4096), (7, 32, 0), (1, 64, 513)])
 def test_group_routes_match_the_oracle(gpu, experts, bm, a):
     """ops::group on the device equals its C restatement bitwise (ids >= experts included)."""
     rng = np.random.default_rng(a + experts)
