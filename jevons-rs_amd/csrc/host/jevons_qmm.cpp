@@ -995,7 +995,7 @@ jv_status jv_group_routes(jv_ctx *ctx, const uint32_t *ids, size_t assignments, 
         return fail(JV_ERR_INVALID, "null buffer");
     uint32_t a = (uint32_t)assignments, e = (uint32_t)experts, b = bm;
     void *args[] = {&ids, &a, &e, &b, &sorted, &offsets, &jobs};
-    return launch(ctx, "jv_group_routes", dim3(1), dim3(512), 0, stream, args);
+    return launch(ctx, "jv_group_routes", dim3(1), dim3(1024), 0, stream, args);
 }
 
 namespace {

@@ -1994,7 +1994,7 @@ JV_PICK(f16, FF16)
 // offsets[e] is expert e's first sorted position (offsets[experts] = routed count), jobs[0] the
 // number of bm-row tiles and jobs[1 + 2j], jobs[2 + 2j] tile j's (expert, first position).
 // Ids >= experts are not routed; experts <= 1024.
-extern "C" __global__ __launch_bounds__(512) void jv_group_routes(const uint32_t *ids, uint32_t assignments,
+extern "C" __global__ __launch_bounds__(1024) void jv_group_routes(const uint32_t *ids, uint32_t assignments,
                                                                   uint32_t experts, uint32_t bm,
                                                                   uint32_t *sorted, uint32_t *offsets,
                                                                   uint32_t *jobs) {
@@ -2003,7 +2003,7 @@ extern "C" __global__ __launch_bounds__(512) void jv_group_routes(const uint32_t
     // positions (expert start + the counts of earlier waves), and the wave places its
     // assignments in order, ranking the lanes of one expert within each 64-assignment batch by
     // ballot. So every expert's positions hold its assignments in increasing order.
-    constexpr int NW = 8;
+    constexpr int NW = 16;
     __shared__ uint32_t cnt[NW][1024];
     __shared__ uint32_t starts[1025], jst[1025];
     const int tid = (int)threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -2029,18 +2029,41 @@ extern "C" __global__ __launch_bounds__(512) void jv_group_routes(const uint32_t
         starts[ex] = sum;
     }
     __syncthreads();
-    if (tid == 0) {
-        uint32_t acc = 0, jacc = 0;
-        for (uint32_t ex = 0; ex < experts; ++ex) {
-            const uint32_t c = starts[ex];
-            starts[ex] = acc;
-            jst[ex] = jacc;
-            acc += c;
-            jacc += (c + bm - 1) / bm;
+    if (wv == 0) {  // exclusive scans of the counts and job counts: lane l owns experts 16l..16l+15
+        uint32_t c[16], jc[16], sum = 0, jsum = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t ex = 16u * (uint32_t)lane + (uint32_t)i;
+            c[i] = ex < experts ? starts[ex] : 0u;
+            jc[i] = (c[i] + bm - 1) / bm;
+            sum += c[i];
+            jsum += jc[i];
         }
-        starts[experts] = acc;
-        offsets[experts] = acc;
-        jobs[0] = jacc;
+        uint32_t incl = sum, jincl = jsum;  // inclusive prefix over lanes
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_up((int)incl, d), jo = (uint32_t)__shfl_up((int)jincl, d);
+            if (lane >= d) {
+                incl += o;
+                jincl += jo;
+            }
+        }
+        uint32_t acc = incl - sum, jacc = jincl - jsum;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t ex = 16u * (uint32_t)lane + (uint32_t)i;
+            if (ex < experts) {
+                starts[ex] = acc;
+                jst[ex] = jacc;
+            }
+            acc += c[i];
+            jacc += jc[i];
+        }
+        if (lane == 63) {
+            starts[experts] = incl;
+            offsets[experts] = incl;
+            jobs[0] = jincl;
+        }
     }
     __syncthreads();
     for (uint32_t ex = (uint32_t)tid; ex < experts; ex += 64 * NW) {
