@@ -1587,7 +1587,7 @@ struct DF {  // any format with the F* interface of the small-tile kernel
 //
 // Each output element is the same MFMA chain over K as in the other tiled kernels (32-k steps
 // in order, lane group g holding k 32s + 8g .. +8), so the result is bitwise identical to theirs.
-template <class D, int TM, int TN, int WM, int WN, bool HB = false, bool APRIV = false>
+template <class D, int TM, int TN, int WM, int WN, bool HB = false, bool APRIV = false, int NVS = 3>
 __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     constexpr int W = WM * WN, MT = TM / WM, NT = TN / WN;
     // activation fragments a wave loads per stage (own m slots): a share of its MT, or with
@@ -1757,7 +1757,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
             constexpr int NM = MT * NT;                       // MFMAs of the stage
             constexpr int NR = (MT - AS) + (NT - BS);         // LDS reads
             constexpr int NW = (ASH ? AS : 0) + BS;           // LDS writes
-            constexpr int NV = 3;                             // VALU per MFMA slot
+            constexpr int NV = NVS;                           // VALU per MFMA slot
 #pragma unroll
             for (int i = 0; i < NM; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
@@ -1812,27 +1812,31 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 // on the 4 x 2 / 2 x 2 grid with each wave loading all of its m-tiles (APRIV, waves of one grid
 // row load the same fragments) and reading only its share of the weights from LDS.
 // Those are the library's tiles for these formats (the faster arrangement per format and tile
-// in interleaved measurements); the same bits either way.
-#define JV_GEMM(NAME, D, TM, TN, WM, WN, ROWS, COLS, SUF, HB)                                 \
+// in interleaved measurements); the same bits either way. The last argument is how many VALU
+// instructions the scheduler places after each MFMA of a stage (the weight decode is spread
+// over the MFMAs): 4 for Q4_K and 5 for Q6_K on 256 x 128 (2 x 8 MFMAs per stage), 1 for the
+// Q4_K 64 x 64 and the Q4_K / Q6_K 128 x 128 tiles, 3 elsewhere, each the fastest of 1 .. 5 in
+// interleaved measurements (3 to 9 % over 3 where it differs).
+#define JV_GEMM(NAME, D, TM, TN, WM, WN, ROWS, COLS, SUF, HB, NV)                             \
     extern "C" __global__ __launch_bounds__(64 * WM * WN) void jv_gemm_##NAME##_##ROWS##x##COLS##SUF(GemmParams p) { \
-        gemm_body<D, TM, TN, WM, WN, HB>(p);                                                  \
+        gemm_body<D, TM, TN, WM, WN, HB, false, NV>(p);                                       \
     }
-#define JV_GEMMP(NAME, D, TM, TN, WM, WN, ROWS, COLS, SUF)                                    \
+#define JV_GEMMP(NAME, D, TM, TN, WM, WN, ROWS, COLS, SUF, NV)                                \
     extern "C" __global__ __launch_bounds__(64 * WM * WN) void jv_gemm_##NAME##_##ROWS##x##COLS##SUF(GemmParams p) { \
-        gemm_body<D, TM, TN, WM, WN, true, true>(p);                                          \
+        gemm_body<D, TM, TN, WM, WN, true, true, NV>(p);                                      \
     }
 #define JV_GEMM_TILES(NAME, D)                                                                \
-    JV_GEMM(NAME, D, 16, 8, 4, 2, 256, 128, , false) JV_GEMM(NAME, D, 8, 8, 4, 2, 128, 128, , false) \
-    JV_GEMM(NAME, D, 4, 4, 2, 2, 64, 64, , false)
-JV_GEMM(q4k, DQ4K, 16, 8, 8, 1, 256, 128, r, true)
-JV_GEMM(q6k, DF<FQ6K>, 16, 8, 8, 1, 256, 128, r, true)
-JV_GEMMP(q8_0, DF<FQ8_0>, 16, 8, 4, 2, 256, 128, r)
-JV_GEMMP(q4k, DQ4K, 4, 4, 2, 2, 64, 64, r)
-JV_GEMMP(q6k, DF<FQ6K>, 4, 4, 2, 2, 64, 64, r)
-JV_GEMMP(q8_0, DF<FQ8_0>, 4, 4, 2, 2, 64, 64, r)
-JV_GEMMP(q4k, DQ4K, 8, 8, 4, 2, 128, 128, r)
-JV_GEMMP(q6k, DF<FQ6K>, 8, 8, 4, 2, 128, 128, r)
-JV_GEMMP(q8_0, DF<FQ8_0>, 8, 8, 4, 2, 128, 128, r)
+    JV_GEMM(NAME, D, 16, 8, 4, 2, 256, 128, , false, 3) JV_GEMM(NAME, D, 8, 8, 4, 2, 128, 128, , false, 3) \
+    JV_GEMM(NAME, D, 4, 4, 2, 2, 64, 64, , false, 3)
+JV_GEMM(q4k, DQ4K, 16, 8, 8, 1, 256, 128, r, true, 4)
+JV_GEMM(q6k, DF<FQ6K>, 16, 8, 8, 1, 256, 128, r, true, 5)
+JV_GEMMP(q8_0, DF<FQ8_0>, 16, 8, 4, 2, 256, 128, r, 3)
+JV_GEMMP(q4k, DQ4K, 4, 4, 2, 2, 64, 64, r, 1)
+JV_GEMMP(q6k, DF<FQ6K>, 4, 4, 2, 2, 64, 64, r, 3)
+JV_GEMMP(q8_0, DF<FQ8_0>, 4, 4, 2, 2, 64, 64, r, 3)
+JV_GEMMP(q4k, DQ4K, 8, 8, 4, 2, 128, 128, r, 1)
+JV_GEMMP(q6k, DF<FQ6K>, 8, 8, 4, 2, 128, 128, r, 1)
+JV_GEMMP(q8_0, DF<FQ8_0>, 8, 8, 4, 2, 128, 128, r, 3)
 JV_GEMM_TILES(q4k, DQ4K)
 JV_GEMM_TILES(q6k, DF<FQ6K>)
 JV_GEMM_TILES(q8_0, DF<FQ8_0>)
