@@ -428,13 +428,18 @@ jv_status launch_tiles(jv_ctx *ctx, const void *x, jv_act act, size_t m, const j
                   stream, rargs);
 }
 
-// Pipelined tile kernels (256 x 128, 128 x 128, 64 x 64; whole K in 256-element blocks):
-// activations -> packed FP16 fragments (per job when grouped), then the product. Every output
-// element is the same MFMA chain as in the generic tile kernel, so the plans give the same bits.
+// Pipelined tile kernels (256 x 128, 128 x 128, 64 x 64, and 32 x 64 for Q4_K, Q6_K and Q8_0;
+// whole K in 256-element blocks): activations -> packed FP16 fragments (per job when grouped),
+// then the product. Every output element is the same MFMA chain as in the generic tile kernel,
+// so the plans give the same bits.
+bool reg_format(const jv_qmatrix *w) {
+    return w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0;
+}
+
 bool pipelined_plan(const jv_qmatrix *w, jv_plan plan) {
     return plan.splits == 1 && w->k % 256 == 0 &&
            ((plan.bm == 256 && plan.bn == 128) || (plan.bm == 128 && plan.bn == 128) ||
-            (plan.bm == 64 && plan.bn == 64));
+            (plan.bm == 64 && plan.bn == 64) || (reg_format(w) && plan.bm == 32 && plan.bn == 64));
 }
 
 jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, const jv_qmatrix *w,
@@ -493,11 +498,9 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     char name[40];
     // Q4_K, Q6_K and Q8_0 tiles run on waves that keep their activation fragments in
     // registers (same bits as the tiles that share them through LDS; JV_GEMM_REG=0 selects
-    // those).
+    // those, except for 32 x 64, which exists only with register fragments).
     const char *regenv = getenv("JV_GEMM_REG");
-    const bool reg = (plan.bm == 256 || plan.bm == 128 || plan.bm == 64) &&
-                     (w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
-                     !(regenv && regenv[0] == '0');
+    const bool reg = reg_format(w) && (plan.bm == 32 || !(regenv && regenv[0] == '0'));
     snprintf(name, sizeof name, "jv_gemm_%s_%ux%u%s", fmt_kernel_name(w->fmt), plan.bm, plan.bn,
              reg ? "r" : "");
     const unsigned waves = plan.bm >= 128 ? 8 : 4;
@@ -900,6 +903,9 @@ jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
             return jv_plan{256, 128, 1};
         if (cols % 128 == 0 && m > 64 && ((m + 127) / 128) * (cols / 128) * 16 >= cus * 15)
             return jv_plan{128, 128, 1};
+        // up to 32 rows: half a 64-row tile would be padding (Q6_K vocabulary projection at
+        // m = 32: 235 us against 281 us on 64 x 64; Q8_0 4096 x 4096: 25 against 29 us)
+        if (cols % 64 == 0 && m <= 32 && reg_format(w)) return jv_plan{32, 64, 1};
         if (cols % 64 == 0) return jv_plan{64, 64, 1};
     }
     const uint32_t bm = m <= 32 ? 32 : (m <= 64 ? 64 : 128);

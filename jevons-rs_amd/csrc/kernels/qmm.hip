@@ -1810,13 +1810,16 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 // the weights, writing stages three ahead with a barrier every second stage (HB): Q4_K and Q6_K
 // 256 x 128 on 8 waves of 8 x 1 (32 x 128 each); Q8_0 256 x 128 and every 128 x 128 and 64 x 64
 // on the 4 x 2 / 2 x 2 grid with each wave loading all of its m-tiles (APRIV, waves of one grid
-// row load the same fragments) and reading only its share of the weights from LDS.
+// row load the same fragments) and reading only its share of the weights from LDS. These three
+// formats also have a 32 x 64 r tile (2 x 2 waves of 16 x 32) for products of up to 32 rows,
+// which a 64-row tile would half fill.
 // Those are the library's tiles for these formats (the faster arrangement per format and tile
 // in interleaved measurements); the same bits either way. The last argument is how many VALU
 // instructions the scheduler places after each MFMA of a stage (the weight decode is spread
 // over the MFMAs): 4 for Q4_K and 5 for Q6_K on 256 x 128 (2 x 8 MFMAs per stage), 1 for the
-// Q4_K 64 x 64 and the Q4_K / Q6_K 128 x 128 tiles, 3 elsewhere, each the fastest of 1 .. 5 in
-// interleaved measurements (3 to 9 % over 3 where it differs).
+// Q4_K 64 x 64 and the Q4_K / Q6_K 128 x 128 tiles, 2 for 32 x 64, 3 elsewhere, each the
+// fastest of 1 .. 5 (1 .. 3 for 32 x 64) in interleaved measurements (3 to 9 % over 3 where it
+// differs).
 #define JV_GEMM(NAME, D, TM, TN, WM, WN, ROWS, COLS, SUF, HB, NV)                             \
     extern "C" __global__ __launch_bounds__(64 * WM * WN) void jv_gemm_##NAME##_##ROWS##x##COLS##SUF(GemmParams p) { \
         gemm_body<D, TM, TN, WM, WN, HB, false, NV>(p);                                       \
@@ -1837,6 +1840,9 @@ JV_GEMMP(q8_0, DF<FQ8_0>, 4, 4, 2, 2, 64, 64, r, 3)
 JV_GEMMP(q4k, DQ4K, 8, 8, 4, 2, 128, 128, r, 1)
 JV_GEMMP(q6k, DF<FQ6K>, 8, 8, 4, 2, 128, 128, r, 1)
 JV_GEMMP(q8_0, DF<FQ8_0>, 8, 8, 4, 2, 128, 128, r, 3)
+JV_GEMMP(q4k, DQ4K, 2, 4, 2, 2, 32, 64, r, 2)
+JV_GEMMP(q6k, DF<FQ6K>, 2, 4, 2, 2, 32, 64, r, 2)
+JV_GEMMP(q8_0, DF<FQ8_0>, 2, 4, 2, 2, 32, 64, r, 2)
 JV_GEMM_TILES(q4k, DQ4K)
 JV_GEMM_TILES(q6k, DF<FQ6K>)
 JV_GEMM_TILES(q8_0, DF<FQ8_0>)

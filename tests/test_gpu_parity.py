@@ -382,8 +382,8 @@ def test_tiled_products_use_the_reference_f16_tile(gpu, name, type_id):
     w, raw = make_matrix(gpu, type_id, n, k, seed=17)
     tile = O.dequantize(type_id, raw).reshape(n, k).astype(np.float16).astype(np.float32)
     x = torch.eye(k, dtype=torch.float16, device="cuda")
-    plans = [jq.Plan(32, 64, 1), jq.Plan(64, 128, 1), jq.Plan(128, 64, 1), jq.Plan(128, 128, 1),
-             jq.Plan(256, 128, 1)]
+    plans = [jq.Plan(32, 64, 1), jq.Plan(32, 128, 1), jq.Plan(64, 64, 1), jq.Plan(64, 128, 1),
+             jq.Plan(128, 64, 1), jq.Plan(128, 128, 1), jq.Plan(256, 128, 1)]
     for plan in [pl for pl in plans if pl.valid_for(w, k)]:
         out = torch.empty((k, n), dtype=torch.float32, device="cuda")
         jq.matmul_plan(gpu, x, k, w, out, None, plan)
@@ -447,9 +447,10 @@ def test_q4k_prefill_gemm_m512_rows(gpu):
     say("plan", plan, "normalized error", e)
     assert e <= TOL
     for r0 in (0, 200, 496):
-        o1 = torch.empty((16, n), dtype=torch.float32, device="cuda")
-        jq.matmul_plan(gpu, x[r0:r0 + 16].contiguous(), 16, w, o1, None, jq.Plan(32, 64, 1))
-        assert torch.equal(o1, out[r0:r0 + 16]), r0
+        for small in (jq.Plan(32, 64, 1), jq.Plan(32, 128, 1)):  # pipelined and generic tiles
+            o1 = torch.empty((16, n), dtype=torch.float32, device="cuda")
+            jq.matmul_plan(gpu, x[r0:r0 + 16].contiguous(), 16, w, o1, None, small)
+            assert torch.equal(o1, out[r0:r0 + 16]), (r0, small)
 
 
 # ------------------------------------------------------------------ expert-grouped products
@@ -531,10 +532,11 @@ def test_grouped_products_of_other_formats(gpu, name, type_id):
 
 @pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0), ("q5_0", jq.Q5_0)])
 def test_grouped_products_on_the_pipelined_tiles(gpu, name, type_id):
-    """Grouped jobs of 64 and 128 rows run on the pipelined tiles (rows gathered per job into
-    packed fragments, the expert's weight rows, scattered output rows). They must give the
-    bits of the generic grouped tiles (32-row jobs) and match the f64 oracle, with experts of
-    several jobs, a partly filled last job and an empty expert; f32 and bf16 outputs."""
+    """Grouped jobs of 32 (Q4_K, Q6_K, Q8_0), 64 and 128 rows run on the pipelined tiles (rows
+    gathered per job into packed fragments, the expert's weight rows, scattered output rows).
+    They must give the bits of the generic grouped tiles (32 x 128 jobs) and match the f64
+    oracle, with experts of several jobs, a partly filled last job and an empty expert; f32
+    and bf16 outputs."""
     experts, n, k, top_k, tokens = 8, 256, 512, 2, 150
     raw = synth.weights(type_id, 51, experts * n, k)
     w = jq.QMatrix.upload(gpu, type_id, n, k, experts, raw)
@@ -545,10 +547,10 @@ def test_grouped_products_on_the_pipelined_tiles(gpu, name, type_id):
     want = O.grouped_product_f64(xv, dense, ids, top_k, n)
     g32 = jq.group_routes(gpu, _i32(ids), experts, 32, in_div=top_k)
     ref = torch.full((ids.size, n), float("nan"), dtype=torch.float32, device="cuda")
-    jq.matmul_grouped(gpu, x, w, g32, ref, 32, 64, 1, None)
+    jq.matmul_grouped(gpu, x, w, g32, ref, 32, 128, 1, None)
     ref = ref.cpu().numpy()
     assert err(ref, want) <= TOL
-    for bm, bn in ((64, 64), (128, 128)):
+    for bm, bn in ((32, 64), (64, 64), (128, 128)):
         g = jq.group_routes(gpu, _i32(ids), experts, bm, in_div=top_k)
         out = torch.full((ids.size, n), float("nan"), dtype=torch.float32, device="cuda")
         jq.matmul_grouped(gpu, x, w, g, out, bm, bn, 1, None)
@@ -788,6 +790,10 @@ def test_plan_rules_follow_the_reference(gpu):
     assert not jq.Plan(128, 128, 0).valid_for(w, 4)
     # the library's own plan: small-row kernel only when rows may differ from the tiles' bits
     assert jq.Plan.auto(w, 4, row_invariant=False).bm == 0
+    # row-invariant products of up to 32 rows take the 32 x 64 tile, up to 64 the 64 x 64 one
+    assert jq.Plan.auto(w, 4, row_invariant=True) == jq.Plan(32, 64, 1)
+    assert jq.Plan.auto(w, 32, row_invariant=True) == jq.Plan(32, 64, 1)
+    assert jq.Plan.auto(w, 40, row_invariant=True) == jq.Plan(64, 64, 1)
     # pipelined tiles by rows on a wide matrix (30720 columns, 240 tile columns of 128): 256 x 128
     # from 192 rows, 128 x 128 above 64 rows, 64 x 64 below, while the workgroups fill the device
     if gpu.info.compute_units == 256:
