@@ -53,6 +53,80 @@ def test_device_decode_is_bit_exact(gpu, name, type_id):
     assert np.array_equal(part.view(np.uint32), want[37:87].view(np.uint32))
 
 
+# FP16 block scales beyond the synthetic ones (bit patterns): signed zeros, the smallest and
+# largest subnormals, +-1, the largest finite values, infinities, NaN, and an ordinary value
+_EXTREME_F16 = np.array([0x0000, 0x8000, 0x0001, 0x83FF, 0x3C00, 0xBC00, 0x7BFF, 0xFBFF, 0x7C00,
+                         0xFC00, 0x7E00, 0x1234], np.uint16)
+# finite ones whose decoded weights stay inside the FP16 range for every format (|d| <= 8)
+_FINITE_F16 = np.array([0x0000, 0x8000, 0x0001, 0x83FF, 0x0400, 0x3C00, 0xBC00, 0xB800, 0xC800], np.uint16)
+_SCALE_FIELDS = {jq.Q4K: (144, (0, 2)), jq.Q6K: (210, (208,)), jq.Q8_0: (34, (0,)), jq.Q5_0: (22, (0,))}
+
+
+def _with_scales(type_id, raw, patterns, seed):
+    """Every block's FP16 scale fields (Q4_K: d and dmin) set to patterns drawn from `patterns`;
+    Q6_K's int8 sub-block scales over their whole range (-128 included)."""
+    rng = np.random.default_rng(seed)
+    bsize, offs = _SCALE_FIELDS[type_id]
+    blocks = raw.reshape(-1, bsize).copy()
+    for o in offs:
+        pick = patterns[rng.integers(0, patterns.size, blocks.shape[0])]
+        blocks[:, o:o + 2] = pick.view(np.uint8).reshape(-1, 2)
+    if type_id == jq.Q6K:
+        blocks[:, 192:208] = rng.integers(0, 256, size=(blocks.shape[0], 16), dtype=np.uint8)
+    return blocks.reshape(-1)
+
+
+def _same_bits_nan_as_nan(got, want, uint):
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan), "NaN positions differ"
+    bad = np.argwhere(got[~nan].view(uint) != want[~nan].view(uint))
+    assert bad.size == 0, f"{bad.size} elements differ"
+
+
+@pytest.mark.parametrize("name,type_id", [f for f in FORMATS if f[1] != jq.F16])
+def test_device_decode_of_extreme_scales(gpu, name, type_id):
+    """Block scales of every FP16 class: the device's FP32 decode equals quant.rs's arithmetic
+    bit for bit (NaN where it is NaN: payloads are not compared), and the FP16 tile is its
+    round to nearest even (overflowing to infinity where the FP32 value is beyond FP16)."""
+    n, k = 64, 1024
+    raw = _with_scales(type_id, synth.weights(type_id, 60, n, k), _EXTREME_F16, 61)
+    w = jq.QMatrix.upload(gpu, type_id, n, k, 1, raw)
+    want = O.dequantize(type_id, raw).reshape(n, k)
+    assert np.isnan(want).any() and np.isinf(want).any()
+    _same_bits_nan_as_nan(jq.dequant_rows(gpu, w, 0, n).cpu().numpy(), want, np.uint32)
+    _same_bits_nan_as_nan(jq.dequant_rows(gpu, w, 0, n, f16=True).cpu().numpy(),
+                          want.astype(np.float16), np.uint16)
+
+
+@pytest.mark.parametrize("name,type_id", [f for f in FORMATS if f[1] != jq.F16])
+def test_products_with_extreme_finite_scales(gpu, name, type_id):
+    """Zero, negative and subnormal block scales through the products: every tiled plan's
+    on-chip tile is the reference's FP16 tile (identity activations), and the small-row and
+    tiled products match the f64 oracle."""
+    n, k = 128, 512
+    raw = _with_scales(type_id, synth.weights(type_id, 62, n, k), _FINITE_F16, 63)
+    w = jq.QMatrix.upload(gpu, type_id, n, k, 1, raw)
+    dense = O.dequantize(type_id, raw).reshape(n, k)
+    assert np.isfinite(dense).all() and (dense < 0).any()
+    tile = dense.astype(np.float16).astype(np.float32)
+    assert np.isfinite(tile).all()
+    x = torch.eye(k, dtype=torch.float16, device="cuda")
+    plans = [jq.Plan(32, 64, 1), jq.Plan(32, 128, 1), jq.Plan(64, 64, 1), jq.Plan(128, 128, 1),
+             jq.Plan(256, 128, 1)]
+    for plan in [pl for pl in plans if pl.valid_for(w, k)]:
+        out = torch.empty((k, n), dtype=torch.float32, device="cuda")
+        jq.matmul_plan(gpu, x, k, w, out, None, plan)
+        got = out.cpu().numpy()
+        want = tile.T.copy() + np.float32(0.0)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), plan
+    scratch = jq.SplitScratch(gpu)
+    for m in (1, 4, 16, 40):
+        xb, xv = activations("bf16", synth.normal_rows(64 + m, m, k))
+        out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        jq.matmul(gpu, xb, m, w, out, scratch)
+        assert err(out.cpu().numpy(), O.matmul_f64(xv, dense)) <= TOL, m
+
+
 def _kats():
     import json
     import os
