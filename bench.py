@@ -120,6 +120,34 @@ def pmc_child():
     print("pmc child done", flush=True)
 
 
+def pmc_gemm_child():
+    """Launch workload of the tiled products' counter passes (run by hand under rocprofv3 --pmc):
+    the Q4_K GEMM M=512 K=3840 N=15360 (256 x 128 tiles), the Q6_K down projection M=256
+    K=15360 N=3840 (64 x 64 tiles) and the Q6_K vocabulary projection M=32 K=3840 N=262144
+    (32 x 64 tiles), ten launches each on two alternating weight copies."""
+    import numpy as np
+    import torch
+
+    import jevons_qmm as jq
+    from jevons_qmm import synth
+
+    gpu = jq.Gpu(0)
+    for fmt, m, n, k, plan in ((jq.Q4K, 512, 15360, 3840, jq.Plan(256, 128, 1)),
+                               (jq.Q6K, 256, 3840, 15360, jq.Plan(64, 64, 1)),
+                               (jq.Q6K, 32, 262144, 3840, jq.Plan(32, 64, 1))):
+        raw_dev = torch.from_numpy(synth.weights(fmt, 2, n, k)).cuda()
+        mats = [jq.QMatrix.upload_device(gpu, fmt, n, k, 1, raw_dev) for _ in range(2)]
+        del raw_dev
+        xb = torch.from_numpy(synth.to_bf16(synth.normal_rows(1, m, k)).view(np.int16).copy())
+        x = xb.view(torch.bfloat16).cuda()
+        out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        for r in range(10):
+            jq.matmul_plan(gpu, x, m, mats[r % 2], out, None, plan)
+        torch.cuda.synchronize()
+        del mats
+    print("pmc child done", flush=True)
+
+
 def _pmc_pass(counter, workdir):
     """One rocprofv3 pass of `counter` over the child workload -> {kernel name: [values]}."""
     prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
@@ -349,7 +377,12 @@ def main():
     ap.add_argument("--no-traffic", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the Q8_0, layer and lm_head lines")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--pmc-gemm", action="store_true",
+                    help="only launch the tiled products (a workload for rocprofv3 --pmc runs)")
     args = ap.parse_args()
+    if args.pmc_gemm:
+        pmc_gemm_child()
+        return
     if args.pmc_child:
         pmc_child()
         return
