@@ -501,9 +501,12 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     // those, except for 32 x 64, which exists only with register fragments).
     const char *regenv = getenv("JV_GEMM_REG");
     const bool reg = reg_format(w) && (plan.bm == 32 || !(regenv && regenv[0] == '0'));
+    // Ungrouped 64 x 64 products run the 8-wave tile (two waves per SIMD); expert jobs keep the
+    // 4-wave one, faster there.
+    const bool w8 = reg && !grp && plan.bm == 64;
     snprintf(name, sizeof name, "jv_gemm_%s_%ux%u%s", fmt_kernel_name(w->fmt), plan.bm, plan.bn,
-             reg ? "r" : "");
-    const unsigned waves = plan.bm >= 128 ? 8 : 4;
+             w8 ? "r8" : (reg ? "r" : ""));
+    const unsigned waves = plan.bm >= 128 || w8 ? 8 : 4;
     const size_t glds = 4 * ((reg ? 0 : plan.bm) + plan.bn) / 16 * 1024;
     return launch(ctx, name, dim3((unsigned)(w->n / plan.bn), (unsigned)jobs_or_tiles),
                   dim3(64 * waves), glds, stream, gargs);

@@ -1717,7 +1717,9 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     // Stages are written LEAD ahead of their MFMAs: 2, with a barrier after every stage, or,
     // with HB (only weights in LDS), 3 with a barrier after every odd stage. Then a buffer
     // written at step t is read at step t + 2 and rewritten at step t + 4, and every such pair
-    // of steps straddles an odd step's barrier.
+    // of steps straddles an odd step's barrier. The one exception is stage 0, read after the
+    // prologue's barrier and rewritten (as stage 4) at step 1: with HB a second barrier follows
+    // that read (each wave's fence waits for its own read to complete first).
     static_assert(!HB || !ASH, "half barriers need activation fragments in registers");
     constexpr int LEAD = HB ? 3 : 2;
 #pragma unroll
@@ -1728,6 +1730,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     }
     lds_barrier();
     read_other(FA[0], FB[0], 0);
+    if constexpr (HB) lds_barrier();
 
     // Stage st (j = st % 8): read stage st + 1's other fragments, MFMAs of stage st, write
     // stage st + LEAD (decode its weight fragments, store its activation fragments), then load
@@ -1804,6 +1807,113 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     }
 }
 
+// 64 x 64 tile on 8 waves, two per SIMD: wave w computes m-tile w / 2 against n-tiles 2 (w % 2)
+// and 2 (w % 2) + 1 (two MFMAs a stage) with its activation fragments in registers, and wave
+// 4 p + q decodes n-tile q's weight fragment of the stages of parity p, so every fragment is
+// still decoded once per workgroup. The stages go through the same four LDS buffers as in
+// gemm_body's HB tiles: written three stages ahead, a barrier after every odd step and one
+// after the prologue's read of stage 0, so a buffer written at step t is read at step t + 2 and
+// rewritten at step t + 4 with a barrier between each pair. Each output element is gemm_body's
+// MFMA chain, so the bits are the same. Two waves per SIMD where the 4-wave tile runs one:
+// down projection 89 against 97 us, q/k/v/o 10-14 % faster. Ungrouped products only: expert
+// jobs (thousands of workgroups, already several per CU) ran slower on it (169 against 149 us
+// on 128 experts x 32 rows).
+template <class D>
+__device__ __forceinline__ void gemm8_body(const GemmParams &p) {
+    constexpr int UPS = 8 / D::SPU;
+    constexpr int LEAD = 3;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, r = lane & 15;
+    const int mq = w >> 1, nh = w & 1;   // compute: m-tile mq, n-tiles 2 nh and 2 nh + 1
+    const int par = w >> 2, dq = w & 3;  // decode: n-tile dq of the stages of parity par
+    const int U8 = p.K >> 8;
+    const int UK = U8 * UPS;
+    const int stages = 8 * U8;
+    const int mt0 = blockIdx.y * 4, t0 = blockIdx.x * 4;
+    const uint32_t lo16 = (uint32_t)lane * 16u;
+    const uint8_t *xa = (const uint8_t *)p.xa + (size_t)(mt0 + mq) * (size_t)stages * 1024u + lo16;
+    auto load_a = [&](u32x4 &dst, int st) __attribute__((always_inline)) {
+        dst = *(const u32x4 *)(xa + (uint32_t)min(st, stages - 1) * 1024u);
+    };
+    auto buf_of = [&](int st) __attribute__((always_inline)) { return smem + (st & 3) * 4096 + lo16; };
+    auto load_w = [&](typename D::Raw *dst, int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < UPS; ++q) D::load(dst[q], p, t0 + dq, min(UPS * b + q, UK - 1), g, r);
+    };
+    typename D::Prep pp[UPS];
+    auto block_prep = [&](const typename D::Raw *it) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < UPS; ++q) D::prep(it[q], pp[q], g);
+    };
+    auto read_b = [&](f16x8 *fb, int st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) fb[k] = *(const f16x8 *)(buf_of(st) + (2 * nh + k) * 1024);
+    };
+    typename D::Raw cur[UPS], nxt[UPS];
+    u32x4 A[4];
+    f16x8 FB[2][2];
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    load_w(cur, 0);
+    load_w(nxt, 1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) load_a(A[t], t);
+    block_prep(cur);
+#pragma unroll
+    for (int t = 0; t < LEAD; ++t)
+        if ((t & 1) == par)
+            *(f16x8 *)(buf_of(t) + dq * 1024) = D::frag(cur[t / D::SPU], pp[t / D::SPU], t % D::SPU, g);
+    lds_barrier();
+    read_b(FB[0], 0);
+    lds_barrier();
+
+    auto step = [&](int st, int j, bool tail) __attribute__((always_inline)) {
+        const int c = j & 3, f = j & 1;
+        const int j2 = (j + LEAD) & 7;
+        if (!tail || st + 1 < stages) read_b(FB[f ^ 1], st + 1);
+        if (!tail || st + LEAD < stages) {
+            if (j2 == 0) {  // stage st + LEAD starts a block of 8: its raw weights are in nxt
+#pragma unroll
+                for (int q = 0; q < UPS; ++q) cur[q] = nxt[q];
+                load_w(nxt, (st + LEAD) / 8 + 1);
+                block_prep(cur);
+            }
+            if ((j2 & 1) == par)
+                *(f16x8 *)(buf_of(st + LEAD) + dq * 1024) =
+                    D::frag(cur[j2 / D::SPU], pp[j2 / D::SPU], j2 % D::SPU, g);
+        }
+        const f16x8 a = __builtin_bit_cast(f16x8, A[c]);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) acc[k] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, FB[f][k], acc[k], 0, 0, 0);
+        load_a(A[c], st + 4);
+        if (j & 1) lds_barrier();
+    };
+    for (int b = 0; b + 1 < U8; ++b) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) step(8 * b + j, j, false);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) step(8 * (U8 - 1) + j, j, true);
+
+    const bool f32_out = p.out_type == 0;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int col = (t0 + 2 * nh + k) * 16 + r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int m = (mt0 + mq) * 16 + 4 * g + e;
+            if (m < p.M) {
+                const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
+                if (f32_out)
+                    ((float *)p.out)[o] = acc[k][e];
+                else
+                    ((uint16_t *)p.out)[o] = (uint16_t)f2bf(acc[k][e]);
+            }
+        }
+    }
+}
+
 // Tiles (rows x columns): 256 x 128 and 128 x 128 on 8 waves of 4 x 2, 64 x 64 on 4 waves of
 // 2 x 2, activation fragments shared through LDS. Q4_K, Q6_K and Q8_0 also have all three tiles
 // with suffix r, whose waves keep their activation fragments in registers, so LDS holds only
@@ -1843,6 +1953,9 @@ JV_GEMMP(q8_0, DF<FQ8_0>, 8, 8, 4, 2, 128, 128, r, 3)
 JV_GEMMP(q4k, DQ4K, 2, 4, 2, 2, 32, 64, r, 2)
 JV_GEMMP(q6k, DF<FQ6K>, 2, 4, 2, 2, 32, 64, r, 2)
 JV_GEMMP(q8_0, DF<FQ8_0>, 2, 4, 2, 2, 32, 64, r, 2)
+extern "C" __global__ __launch_bounds__(512) void jv_gemm_q4k_64x64r8(GemmParams p) { gemm8_body<DQ4K>(p); }
+extern "C" __global__ __launch_bounds__(512) void jv_gemm_q6k_64x64r8(GemmParams p) { gemm8_body<DF<FQ6K>>(p); }
+extern "C" __global__ __launch_bounds__(512) void jv_gemm_q8_0_64x64r8(GemmParams p) { gemm8_body<DF<FQ8_0>>(p); }
 JV_GEMM_TILES(q4k, DQ4K)
 JV_GEMM_TILES(q6k, DF<FQ6K>)
 JV_GEMM_TILES(q8_0, DF<FQ8_0>)
