@@ -369,6 +369,31 @@ def test_register_activation_tiles_equal_the_lds_tiles(gpu, monkeypatch, name, t
         assert np.array_equal(outs[0], o)
 
 
+@pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0)])
+@pytest.mark.parametrize("k", [256, 512])
+def test_eight_wave_tile_short_k_and_bf16_output(gpu, monkeypatch, name, type_id, k):
+    """The 8-wave 64 x 64 tile (weight decode split by stage parity) at K of one and two blocks
+    of 8 stages (the tail alone, one block switch) with a ragged last row tile: the bits of the
+    4-wave tile that shares activations through LDS, the f64 oracle, and a bf16 output equal to
+    the f32 result rounded."""
+    n, m = 192, 70
+    w, raw = make_matrix(gpu, type_id, n, k, seed=71)
+    x, xv = activations("bf16", synth.normal_rows(72, m, k))
+    plan = jq.Plan(64, 64, 1)
+    outs = {}
+    for flag in ("1", "0"):
+        monkeypatch.setenv("JV_GEMM_REG", flag)
+        out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matmul_plan(gpu, x, m, w, out, None, plan)
+        outs[flag] = out
+    assert torch.equal(outs["1"], outs["0"])
+    assert err(outs["1"].cpu().numpy(), oracle_product(type_id, raw, n, k, xv)) <= TOL
+    monkeypatch.setenv("JV_GEMM_REG", "1")
+    o16 = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+    jq.matmul_plan(gpu, x, m, w, o16, None, plan)
+    assert torch.equal(outs["1"].to(torch.bfloat16), o16)
+
+
 def test_wide_matrix_rows_do_not_depend_on_m_when_the_persistent_kernel_does_not_fit(gpu):
     """A wide Q6_K matrix (8 tiles of 16 rows per compute unit) at K = 3840: the persistent
     small-row kernel's LDS fits up to m = 8 but not at m = 16, where the library takes the
