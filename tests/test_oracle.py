@@ -215,19 +215,21 @@ def test_q6k_zero_point_and_sign_of_scales(oracle):
     qh = [0b10101010] * 64
     w = oracle.dequantize(oracle.Q6K, q6k_block(ql, qh, [1] * 16, 1.0))
     assert np.array_equal(w, np.zeros(256, np.float32))
-    # one element at a time with distinct scales: w = d * sc[e // 16] * (q6 - 32)
+    # one element at a time with distinct scales: w = d * sc[e // 16] * (q6 - 32). The high
+    # bits take every value, three of them unlike the background's 2, so an element read from
+    # the wrong qh bits (or a neighbour given this one's) decodes wrong.
     scales = [(-1) ** g * (g + 1) for g in range(16)]
-    for e in [0, 15, 16, 33, 70, 95, 127, 128, 161, 200, 255]:
-        ql = [0] * 128
-        qh = [0b10101010] * 64
-        b, sh, hb, hsh = q6_element_position(e)
-        q6 = 45  # low nibble 13, high bits 2
-        ql[b] |= (q6 & 15) << sh
-        qh[hb] = (qh[hb] & ~(3 << hsh)) | ((q6 >> 4) << hsh)
-        w = oracle.dequantize(oracle.Q6K, q6k_block(ql, qh, scales, 0.5))
-        want = np.zeros(256, np.float32)
-        want[e] = 0.5 * scales[e // 16] * (q6 - 32)
-        assert np.array_equal(w, want), e
+    for q6 in (45, 61, 13, 29):  # low nibble 13, high bits 2, 3, 0, 1
+        for e in [0, 15, 16, 33, 70, 95, 127, 128, 161, 200, 255]:
+            ql = [0] * 128
+            qh = [0b10101010] * 64
+            b, sh, hb, hsh = q6_element_position(e)
+            ql[b] |= (q6 & 15) << sh
+            qh[hb] = (qh[hb] & ~(3 << hsh)) | ((q6 >> 4) << hsh)
+            w = oracle.dequantize(oracle.Q6K, q6k_block(ql, qh, scales, 0.5))
+            want = np.zeros(256, np.float32)
+            want[e] = 0.5 * scales[e // 16] * (q6 - 32)
+            assert np.array_equal(w, want), (q6, e)
 
 
 def test_q5_0_high_bits_follow_qh_bit_order(oracle):
