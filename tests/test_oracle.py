@@ -372,3 +372,21 @@ def test_softcap_is_a_smooth_clamp(oracle):
     assert np.allclose(got, -oracle.softcap(-v, cap), rtol=0, atol=0)
     assert abs(got[4] - 1e-3) < 1e-12 and np.all(np.abs(got) <= cap)
     assert cap - got[-1] < 1e-9 and abs(got[5] - 30.0 * np.tanh(0.5)) < 1e-12
+
+
+def test_pick_logits_is_the_softcapped_product_at_each_pair(oracle):
+    """pick_logits (gpu/ops.rs:589-634): the logit of pair (row, token) is softcap(x[row] .
+    E[token]). A hand example, and every pair of a non-square case against the f64 product,
+    so that swapped pair roles or a transposed table fail."""
+    x = np.array([[1.0, 2.0]], np.float32)
+    table = np.array([[3.0, 4.0], [5.0, 6.0], [7.0, 8.0]], np.float32)
+    got = oracle.pick_logits_f64(x, table, np.array([[0, 1], [0, 2]]), 1e9)
+    assert np.allclose(got, [17.0, 23.0], rtol=1e-12, atol=0)
+    assert abs(oracle.pick_logits_f64(x, table, np.array([[0, 0]]), 10.0)[0] - 10.0 * np.tanh(1.1)) < 1e-12
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((3, 8)).astype(np.float32)
+    table = rng.standard_normal((5, 8)).astype(np.float32)
+    pairs = np.array([[0, 4], [2, 1], [1, 1], [2, 4], [0, 0]])
+    full = oracle.softcap(oracle.matmul_f64(x, table), 30.0)
+    got = oracle.pick_logits_f64(x, table, pairs, 30.0)
+    assert np.allclose(got, [full[r, t] for r, t in pairs], rtol=0, atol=1e-12)
