@@ -215,8 +215,9 @@ def measure_configs(gpu, steps):
     """Kernel durations of the other product configurations, each against its roofline:
     Q8_0 GEMV (M=1, K=N=4096; weights rotated), the six layer GEMMs of one transformer block at
     M=256 (Q4_K q/k/v/o/gate_up, Q6_K down), the Q6_K vocabulary projection (K=3840,
-    N=262144, M = 1, 8, 32) with the per-row argmax of its logits, and an expert-grouped
-    Q4_K product (the routing step's gate/up shape)."""
+    N=262144, M = 1, 8, 32) with the per-row argmax of its logits, and the expert-grouped
+    Q4_K products of the routing step's gate/up shape at prefill (512 tokens) and at decode
+    (8 tokens)."""
     import numpy as np
     import torch
 
@@ -318,8 +319,34 @@ def measure_configs(gpu, steps):
                           "weight_GBps": round(raw.size / (t * 1e-3) / 1e9, 1),
                           "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                                        "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}}
-    del w
+    # decode-time expert product: 8 tokens routed to 8 of the 128 experts each (64 assignments,
+    # one or two rows per touched expert) on the small-row grouped path (jobs of up to 2 rows),
+    # timed over weight copies that together exceed the last-level cache
+    tokens_d = 8
+    route_d = np.stack([rng.choice(experts, top_k, replace=False) for _ in range(tokens_d)]).reshape(-1)
+    touched = len(set(route_d.tolist()))
+    tbytes = touched * (raw.size // experts)
+    copies = max(2, math.ceil(ROTATION_BYTES / tbytes))
+    raw_dev = torch.from_numpy(raw).cuda()
+    wd = [w] + [jq.QMatrix.upload_device(gpu, jq.Q4K, n, k, experts, raw_dev) for _ in range(copies - 1)]
+    del raw_dev
+    ids_d = torch.from_numpy(route_d.astype(np.int32)).cuda()
+    xd = xrows(tokens_d, k, 9)
+    outd = torch.empty((tokens_d * top_k, n), dtype=torch.float32, device="cuda")
+    gd = jq.group_routes(gpu, ids_d, experts, 2, in_div=top_k)
+    jq.matvec_grouped(gpu, xd, w, gd, outd, 2)
+    t = kernel_time_ms(lambda r: jq.matvec_grouped(gpu, xd, wd[r % copies], gd, outd, 2), max(4, steps // 10))
+    gbs = tbytes / (t * 1e-3) / 1e9
+    res["moe_grouped_decode"] = {"workload": f"Q4_K expert-grouped small-row product, {experts} experts N={n} K={k}, "
+                                             f"{tokens_d} tokens x top-{top_k} ({touched} experts touched), "
+                                             "jobs of up to 2 rows, bf16 activations, f32 out",
+                                 "kernel_us": round(t * 1e3, 2), "weight_bytes_touched": tbytes,
+                                 "rotation_copies": copies,
+                                 "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                              "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    del w, wd
     log("moe grouped:", res["moe_grouped"])
+    log("moe grouped decode:", res["moe_grouped_decode"])
     return res
 
 

@@ -1062,6 +1062,53 @@ jv_status jv_matvec_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len
     if (st != JV_OK) return st;
     if (mr == 0 || mr > 16) return fail(JV_ERR_INVALID, "matvec_grouped handles 1 to 16 rows per job");
     if (g->rows == 0 || g->max_jobs == 0) return JV_OK;
+    // Q4_K, Q6_K and Q8_0 jobs run the small-row per-tile kernel in grouped mode (grid y = job),
+    // which streams each job's expert weights as the decode GEMV does; its LDS holds mr rows.
+    // 128 experts [1408, 2816], 8 tokens x top-8: 32 us at mr = 2 (3.7 TB/s of touched expert
+    // weights) against 42 us on the generic grouped tiles; 39 / 41 / 67 against 49 / 42 / 86 us
+    // at mr = 1 / 4 / 16. JV_QMVG=0 takes the generic tiles (tests, measurements).
+    const char *genv = getenv("JV_QMVG");
+    if ((w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
+        w->n * w->experts * w->k < (1ull << 32) && !(genv && genv[0] == '0')) {
+        const bool q8 = w->fmt == JV_FMT_Q8_0, q6 = w->fmt == JV_FMT_Q6K;
+        const int waves = q8 ? 16 : 8;
+        const int ku = q8 ? 64 : 256;  // K per item
+        const int xg = q6 ? 16 : 32;   // columns per activation sum
+        const int U = (int)(w->k / ku);
+        const int umax = (U + waves - 1) / waves;
+        // per wave, as the kernel computes it: FP16 activations [mr][ku umax + 8], sums
+        // [mr][ku umax / xg], a zero row for Q6_K; at least the 1 KB of the tile partial
+        const size_t row = ((size_t)umax * ku + 8) * 2;
+        const size_t stage = ((size_t)mr * row + (size_t)mr * umax * (ku / xg) * 4 + (q6 ? row : 0) + 15) &
+                             ~(size_t)15;
+        const size_t lds = std::max(stage, (size_t)1024) * waves;
+        if (lds <= ctx->info.lds_bytes) {
+            QmmParams p{};
+            p.x = x;
+            p.out = out;
+            p.wq = w->q;
+            p.M = (int32_t)mr;
+            p.N = (int32_t)(w->n);
+            p.K = (int32_t)w->k;
+            p.ldx = (int32_t)w->k;
+            p.ldo = (int32_t)(w->n);
+            p.act = (int32_t)act;
+            p.out_type = (int32_t)out_type;
+            p.splits = 1;
+            p.ids = g->ids;
+            p.offsets = g->offsets;
+            p.jobs = g->jobs;
+            p.grouped = 1;
+            p.in_div = (int32_t)g->in_div;
+            p.rows_cap = (int32_t)mr;
+            void *args[] = {&p};
+            char name[32];
+            const int mv = mr == 1 ? 1 : (mr == 2 ? 2 : 4);
+            snprintf(name, sizeof name, "jv_qmvg_%s_m%d", q8 ? "q8_0" : (q6 ? "q6k" : "q4k"), mv);
+            return launch(ctx, name, dim3((unsigned)(w->n / 16), (unsigned)g->max_jobs), dim3(64 * waves),
+                          lds, stream, args);
+        }
+    }
     GroupArgs ga{g->ids, g->offsets, g->jobs, g->max_jobs, g->in_div, mr};
     return launch_tiles(ctx, x, act, g->rows, w, out, out_type, nullptr, jv_plan{16, 64, 1}, stream,
                         &ga);

@@ -632,7 +632,7 @@ __device__ __forceinline__ uint4 q4k_head_gather(uint32_t hv) {
 // xs[r * stride + c] and FP32 sums of each XG-column group (16 or 32) into Xs[r * xstride + c / XG].
 // The wave's first XB 16-byte loads per lane are issued before `after()` (the weight loads),
 // so waiting for them does not wait for the weights; later batches, if any, come after.
-template <int ACT, int XB, int XG, class After>
+template <int ACT, int XB, int XG, bool GRP = false, class After>
 __device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int ncols, _Float16 *xs,
                                                 int stride, float *Xs, int xstride, int lane,
                                                 After after) {
@@ -657,7 +657,10 @@ __device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int 
             const int c8 = i - r * per_row;
             rq[q] = r;
             cq[q] = c8;
-            const size_t src = (size_t)r * (size_t)p.ldx + (size_t)(c0 + 8 * c8);
+            // expert-grouped: row r of the job is input row ids[r] / in_div (ids = the job's first
+            // sorted position)
+            const int xr = GRP ? (int)(p.ids[r] / (uint32_t)p.in_div) : r;
+            const size_t src = (size_t)xr * (size_t)p.ldx + (size_t)(c0 + 8 * c8);
 #pragma unroll
             for (int hh = 0; hh < LPC; ++hh) {
                 if (ACT == 2)
@@ -1034,8 +1037,8 @@ struct GQ6K {
 // region; after one barrier, wave t adds tile t's W partials in wave order. Each output element
 // is the same sum for every M and TW. Many short workgroups keep every compute unit fed as the
 // memory system serves them unevenly.
-template <class G, int W, int TW, int P, int MV, int XB>
-__device__ __forceinline__ void qmv_body(const QmmParams &p) {
+template <class G, int W, int TW, int P, int MV, int XB, bool GRP = false>
+__device__ __forceinline__ void qmv_body(const QmmParams &p, int wt_off = 0) {
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1063,7 +1066,7 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p) {
     auto load_item = [&](typename G::Item &dst, int idx) {
         idx = min(idx, nitems - 1);
         const int tw = idx / nu;
-        G::load(dst, p, tile0 + tw, u0 + (idx - tw * nu), g, r16);
+        G::load(dst, p, wt_off + tile0 + tw, u0 + (idx - tw * nu), g, r16);
     };
     f32x4 acc[TW];
 #pragma unroll
@@ -1078,11 +1081,11 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p) {
         if (G::kZeroRow)
             for (int i = lane; i < stride / 8; i += 64) *(f16x8 *)(zrow + 8 * i) = f16x8{};
         if (p.act == 0)
-            stage_wave_cols<0, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
+            stage_wave_cols<0, XB, G::XG, GRP>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
         else if (p.act == 1)
-            stage_wave_cols<1, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
+            stage_wave_cols<1, XB, G::XG, GRP>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
         else
-            stage_wave_cols<2, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
+            stage_wave_cols<2, XB, G::XG, GRP>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
         // LDS operations of one wave complete in order; this keeps the compiler from moving
         // the fragment reads above the staging writes.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1128,7 +1131,8 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p) {
         for (int i = 0; i < 4; ++i) {
             const int m = 4 * g + i;
             if (m < p.M) {
-                const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
+                const int mo = GRP ? (int)p.ids[m] : m;  // grouped: output row ids[s]
+                const size_t o = (size_t)mo * (size_t)p.ldo + (size_t)col;
                 if (p.out_type == 0)
                     ((float *)p.out)[o] = sum[i];
                 else
@@ -1416,6 +1420,31 @@ JV_QMVP(q8_0, GQ8_0, 16, 4, 8)
 JV_QMV8(1, 1, 2)
 JV_QMV8(1, 2, 4)
 JV_QMV8(2, 4, 8)
+
+// Expert-grouped small-row kernels (matvec_grouped, gemm.rs:1171-1203): grid y is the job, one
+// 16-row weight tile of the job's expert per workgroup; the job's rows (at most rows_cap) are
+// its sorted positions, read from input rows ids[s] / in_div and written to output rows
+// ids[s]. Unused job slots return before any barrier.
+#define JV_QMVG(NAME, G, W, P, MV, XB)                                                        \
+    extern "C" __global__ __launch_bounds__(64 * W) void jv_qmvg_##NAME##_m##MV(QmmParams p) { \
+        const int job = blockIdx.y;                                                           \
+        if (job >= (int)p.jobs[0]) return;                                                    \
+        const uint32_t e = p.jobs[1 + 2 * job];                                               \
+        const int js = (int)p.jobs[2 + 2 * job];                                              \
+        QmmParams q = p;                                                                      \
+        q.M = min((int)(p.offsets[e + 1] - (uint32_t)js), p.rows_cap);                        \
+        q.ids = p.ids + js;                                                                   \
+        qmv_body<G, W, 1, P, MV, XB, true>(q, (int)e * (p.N >> 4));                           \
+    }
+JV_QMVG(q4k, GQ4K, 8, 2, 1, 2)
+JV_QMVG(q4k, GQ4K, 8, 2, 2, 4)
+JV_QMVG(q4k, GQ4K, 8, 2, 4, 8)
+JV_QMVG(q6k, GQ6K, 8, 2, 1, 2)
+JV_QMVG(q6k, GQ6K, 8, 2, 2, 4)
+JV_QMVG(q6k, GQ6K, 8, 2, 4, 8)
+JV_QMVG(q8_0, GQ8_0, 16, 4, 1, 2)
+JV_QMVG(q8_0, GQ8_0, 16, 4, 2, 4)
+JV_QMVG(q8_0, GQ8_0, 16, 4, 4, 8)
 
 // Split-K kernels: W tiles x one K slice per workgroup (activation staging shared by the waves).
 #define JV_QMVS(NAME, G, W, P, MV, XB, WPE)                                                  \

@@ -629,6 +629,35 @@ def test_grouped_products_of_other_formats(gpu, name, type_id):
         assert e <= (TOL if out_dtype == torch.float32 else 8e-3), (out_dtype, e)
 
 
+@pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0)])
+def test_small_row_grouped_products(gpu, monkeypatch, name, type_id):
+    """matvec_grouped on the small-row kernels in grouped mode (grid y = job; rows gathered from
+    ids / in_div, the expert's weight tiles, output rows scattered to ids): jobs of 1, 2, 4 and
+    16 rows, uneven expert loads with an empty expert, K of several items per wave, f32 and
+    bf16 outputs, against the f64 oracle and the generic grouped tiles (JV_QMVG=0)."""
+    experts, n, k, top_k, tokens = 8, 192, 3840 if type_id != jq.Q8_0 else 4096, 2, 21
+    raw = synth.weights(type_id, 81, experts * n, k)
+    w = jq.QMatrix.upload(gpu, type_id, n, k, experts, raw)
+    dense = O.dequantize(type_id, raw).reshape(experts * n, k)
+    x, xv = activations("bf16", synth.normal_rows(82, tokens, k))
+    rng = np.random.default_rng(83)
+    ids = rng.choice([0, 1, 1, 2, 3, 3, 3, 5, 6, 7], tokens * top_k).astype(np.uint32)  # expert 4 empty
+    want = O.grouped_product_f64(xv, dense, ids, top_k, n)
+    for mr in (1, 2, 4, 16):
+        g = jq.group_routes(gpu, _i32(ids), experts, mr, in_div=top_k)
+        outs = {}
+        for flag in ("1", "0"):
+            monkeypatch.setenv("JV_QMVG", flag)
+            out = torch.full((ids.size, n), float("nan"), dtype=torch.float32, device="cuda")
+            jq.matvec_grouped(gpu, x, w, g, out, mr)
+            outs[flag] = out.cpu().numpy()
+            assert err(outs[flag], want) <= TOL, (mr, flag)
+        monkeypatch.setenv("JV_QMVG", "1")
+        o16 = torch.zeros((ids.size, n), dtype=torch.bfloat16, device="cuda")
+        jq.matvec_grouped(gpu, x, w, g, o16, mr)
+        assert err(o16.float().cpu().numpy(), want) <= 8e-3, mr
+
+
 @pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0), ("q5_0", jq.Q5_0)])
 def test_grouped_products_on_the_pipelined_tiles(gpu, name, type_id):
     """Grouped jobs of 32 (Q4_K, Q6_K, Q8_0), 64 and 128 rows run on the pipelined tiles (rows
