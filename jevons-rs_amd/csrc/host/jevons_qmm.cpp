@@ -1064,9 +1064,10 @@ jv_status jv_matvec_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len
     if (g->rows == 0 || g->max_jobs == 0) return JV_OK;
     // Q4_K, Q6_K and Q8_0 jobs run the small-row per-tile kernel in grouped mode (grid y = job),
     // which streams each job's expert weights as the decode GEMV does; its LDS holds mr rows.
+    // Jobs of more than 2 rows go through in chunks of 2, so the LDS holds at most 2 rows
+    // (8 tokens x top-8 at mr = 16: 37 us against 85 us on the generic tiles).
     // 128 experts [1408, 2816], 8 tokens x top-8: 32 us at mr = 2 (3.7 TB/s of touched expert
-    // weights) against 42 us on the generic grouped tiles; 39 / 41 / 67 against 49 / 42 / 86 us
-    // at mr = 1 / 4 / 16. JV_QMVG=0 takes the generic tiles (tests, measurements).
+    // weights) against 42 us on the generic grouped tiles. JV_QMVG=0 takes the generic tiles.
     const char *genv = getenv("JV_QMVG");
     if ((w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
         w->n * w->experts * w->k < (1ull << 32) && !(genv && genv[0] == '0')) {
@@ -1076,11 +1077,11 @@ jv_status jv_matvec_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len
         const int xg = q6 ? 16 : 32;   // columns per activation sum
         const int U = (int)(w->k / ku);
         const int umax = (U + waves - 1) / waves;
-        // per wave, as the kernel computes it: FP16 activations [mr][ku umax + 8], sums
-        // [mr][ku umax / xg], a zero row for Q6_K; at least the 1 KB of the tile partial
+        // per wave, as the kernel computes it: FP16 activations [mv][ku umax + 8], sums
+        // [mv][ku umax / xg], a zero row for Q6_K; at least the 1 KB of the tile partial
+        const size_t mv = mr == 1 ? 1 : 2;  // rows per chunk
         const size_t row = ((size_t)umax * ku + 8) * 2;
-        const size_t stage = ((size_t)mr * row + (size_t)mr * umax * (ku / xg) * 4 + (q6 ? row : 0) + 15) &
-                             ~(size_t)15;
+        const size_t stage = (mv * row + mv * umax * (ku / xg) * 4 + (q6 ? row : 0) + 15) & ~(size_t)15;
         const size_t lds = std::max(stage, (size_t)1024) * waves;
         if (lds <= ctx->info.lds_bytes) {
             QmmParams p{};
@@ -1103,8 +1104,8 @@ jv_status jv_matvec_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len
             p.rows_cap = (int32_t)mr;
             void *args[] = {&p};
             char name[32];
-            const int mv = mr == 1 ? 1 : (mr == 2 ? 2 : 4);
-            snprintf(name, sizeof name, "jv_qmvg_%s_m%d", q8 ? "q8_0" : (q6 ? "q6k" : "q4k"), mv);
+            snprintf(name, sizeof name, "jv_qmvg_%s_%s", q8 ? "q8_0" : (q6 ? "q6k" : "q4k"),
+                     mr == 1 ? "m1" : (mr == 2 ? "m2" : "c2"));
             return launch(ctx, name, dim3((unsigned)(w->n / 16), (unsigned)g->max_jobs), dim3(64 * waves),
                           lds, stream, args);
         }

@@ -1424,27 +1424,47 @@ JV_QMV8(2, 4, 8)
 // Expert-grouped small-row kernels (matvec_grouped, gemm.rs:1171-1203): grid y is the job, one
 // 16-row weight tile of the job's expert per workgroup; the job's rows (at most rows_cap) are
 // its sorted positions, read from input rows ids[s] / in_div and written to output rows
-// ids[s]. Unused job slots return before any barrier.
+// ids[s]. Unused job slots return before any barrier. Jobs of more than 2 rows go through in
+// chunks of 2 rows (_c2), a barrier between chunks (the next chunk's staging reuses the LDS the
+// partials were read from), so the LDS holds 2 rows whatever rows_cap is; a later chunk reads
+// the tile again, from L2. Jobs of 1 or 2 rows take the single-pass kernels (_m1, _m2), which
+// need fewer registers.
+#define JV_QMVG_HEAD                                                                          \
+    const int job = blockIdx.y;                                                               \
+    if (job >= (int)p.jobs[0]) return;                                                        \
+    const uint32_t e = p.jobs[1 + 2 * job];                                                   \
+    const int js = (int)p.jobs[2 + 2 * job];                                                  \
+    const int rows = min((int)(p.offsets[e + 1] - (uint32_t)js), p.rows_cap);
+// jobs of at most MV rows (rows_cap <= MV): one pass
 #define JV_QMVG(NAME, G, W, P, MV, XB)                                                        \
     extern "C" __global__ __launch_bounds__(64 * W) void jv_qmvg_##NAME##_m##MV(QmmParams p) { \
-        const int job = blockIdx.y;                                                           \
-        if (job >= (int)p.jobs[0]) return;                                                    \
-        const uint32_t e = p.jobs[1 + 2 * job];                                               \
-        const int js = (int)p.jobs[2 + 2 * job];                                              \
+        JV_QMVG_HEAD                                                                          \
         QmmParams q = p;                                                                      \
-        q.M = min((int)(p.offsets[e + 1] - (uint32_t)js), p.rows_cap);                        \
+        q.M = rows;                                                                           \
         q.ids = p.ids + js;                                                                   \
         qmv_body<G, W, 1, P, MV, XB, true>(q, (int)e * (p.N >> 4));                           \
     }
+// jobs of more rows: chunks of 2
+#define JV_QMVGC(NAME, G, W, P)                                                               \
+    extern "C" __global__ __launch_bounds__(64 * W) void jv_qmvg_##NAME##_c2(QmmParams p) {   \
+        JV_QMVG_HEAD                                                                          \
+        for (int r0 = 0; r0 < rows; r0 += 2) {                                                \
+            if (r0 > 0) lds_barrier();                                                        \
+            QmmParams q = p;                                                                  \
+            q.M = min(2, rows - r0);                                                          \
+            q.ids = p.ids + js + r0;                                                          \
+            qmv_body<G, W, 1, P, 2, 4, true>(q, (int)e * (p.N >> 4));                         \
+        }                                                                                     \
+    }
 JV_QMVG(q4k, GQ4K, 8, 2, 1, 2)
 JV_QMVG(q4k, GQ4K, 8, 2, 2, 4)
-JV_QMVG(q4k, GQ4K, 8, 2, 4, 8)
+JV_QMVGC(q4k, GQ4K, 8, 2)
 JV_QMVG(q6k, GQ6K, 8, 2, 1, 2)
 JV_QMVG(q6k, GQ6K, 8, 2, 2, 4)
-JV_QMVG(q6k, GQ6K, 8, 2, 4, 8)
+JV_QMVGC(q6k, GQ6K, 8, 2)
 JV_QMVG(q8_0, GQ8_0, 16, 4, 1, 2)
 JV_QMVG(q8_0, GQ8_0, 16, 4, 2, 4)
-JV_QMVG(q8_0, GQ8_0, 16, 4, 4, 8)
+JV_QMVGC(q8_0, GQ8_0, 16, 4)
 
 // Split-K kernels: W tiles x one K slice per workgroup (activation staging shared by the waves).
 #define JV_QMVS(NAME, G, W, P, MV, XB, WPE)                                                  \
