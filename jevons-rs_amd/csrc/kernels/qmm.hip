@@ -1461,12 +1461,14 @@ JV_QMV8(2, 4, 8)
 JV_QMVG(q4k, GQ4K, 4, 3, 1, 2)
 JV_QMVG(q4k, GQ4K, 4, 3, 2, 4)
 JV_QMVGC(q4k, GQ4K, 4, 3)
-JV_QMVG(q6k, GQ6K, 8, 2, 1, 2)
-JV_QMVG(q6k, GQ6K, 8, 2, 2, 4)
-JV_QMVGC(q6k, GQ6K, 8, 2)
-JV_QMVG(q8_0, GQ8_0, 16, 4, 1, 2)
-JV_QMVG(q8_0, GQ8_0, 16, 4, 2, 4)
-JV_QMVGC(q8_0, GQ8_0, 16, 4)
+// Q6_K on 4 waves, Q8_0 on 8 (the per-tile kernels' 8 and 16 waves: 13-14 % and 31-34 % slower
+// on the same expert shapes in Q6_K and Q8_0)
+JV_QMVG(q6k, GQ6K, 4, 3, 1, 2)
+JV_QMVG(q6k, GQ6K, 4, 3, 2, 4)
+JV_QMVGC(q6k, GQ6K, 4, 3)
+JV_QMVG(q8_0, GQ8_0, 8, 8, 1, 2)
+JV_QMVG(q8_0, GQ8_0, 8, 8, 2, 4)
+JV_QMVGC(q8_0, GQ8_0, 8, 8)
 
 // Split-K kernels: W tiles x one K slice per workgroup (activation staging shared by the waves).
 #define JV_QMVS(NAME, G, W, P, MV, XB, WPE)                                                  \
