@@ -1072,7 +1072,7 @@ jv_status jv_matvec_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len
     if ((w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
         w->n * w->experts * w->k < (1ull << 32) && !(genv && genv[0] == '0')) {
         const bool q8 = w->fmt == JV_FMT_Q8_0, q6 = w->fmt == JV_FMT_Q6K;
-        const int waves = q8 ? 8 : 4;  // as the jv_qmvg_* kernels are built
+        const int waves = 4;  // as the jv_qmvg_* kernels are built
         const int ku = q8 ? 64 : 256;  // K per item
         const int xg = q6 ? 16 : 32;   // columns per activation sum
         const int U = (int)(w->k / ku);

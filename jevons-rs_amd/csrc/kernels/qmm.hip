@@ -1461,14 +1461,15 @@ JV_QMV8(2, 4, 8)
 JV_QMVG(q4k, GQ4K, 4, 3, 1, 2)
 JV_QMVG(q4k, GQ4K, 4, 3, 2, 4)
 JV_QMVGC(q4k, GQ4K, 4, 3)
-// Q6_K on 4 waves, Q8_0 on 8 (the per-tile kernels' 8 and 16 waves: 13-14 % and 31-34 % slower
-// on the same expert shapes in Q6_K and Q8_0)
+// Q6_K and Q8_0 on 4 waves too (Q8_0 with 12 of its 64-k items in flight per wave). On the
+// same expert shapes, the per-tile kernels' 8 waves (Q6_K) were 13-14 % slower; Q8_0's 16
+// waves took 87 / 223 us and 8 waves 58 / 152 us against 48 / 119 us on 4 (8 / 32 tokens).
 JV_QMVG(q6k, GQ6K, 4, 3, 1, 2)
 JV_QMVG(q6k, GQ6K, 4, 3, 2, 4)
 JV_QMVGC(q6k, GQ6K, 4, 3)
-JV_QMVG(q8_0, GQ8_0, 8, 8, 1, 2)
-JV_QMVG(q8_0, GQ8_0, 8, 8, 2, 4)
-JV_QMVGC(q8_0, GQ8_0, 8, 8)
+JV_QMVG(q8_0, GQ8_0, 4, 12, 1, 2)
+JV_QMVG(q8_0, GQ8_0, 4, 12, 2, 4)
+JV_QMVGC(q8_0, GQ8_0, 4, 12)
 
 // Split-K kernels: W tiles x one K slice per workgroup (activation staging shared by the waves).
 #define JV_QMVS(NAME, G, W, P, MV, XB, WPE)                                                  \
