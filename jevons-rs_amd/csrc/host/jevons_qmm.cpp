@@ -142,6 +142,9 @@ struct jv_ctx {
     void *pack = nullptr;  // packed activation fragments of the pipelined tiles (grows)
     size_t pack_bytes = 0;
     jv_scratch *own = nullptr;  // split-K small-row scratch of products given none (grows)
+    // Buffers replaced by a larger one. A HIP graph captured before the growth still holds their
+    // addresses, so they stay allocated until the context is closed.
+    std::vector<void *> retired;
 };
 
 struct jv_qmatrix {
@@ -158,6 +161,7 @@ struct jv_scratch {
     jv_ctx *ctx = nullptr;
     void *buf = nullptr;
     size_t bytes = 0;
+    std::vector<void *> retired;  // smaller buffers kept for graphs captured on them
 };
 
 namespace {
@@ -167,17 +171,27 @@ namespace {
 constexpr size_t kCounterTiles = 65536;
 constexpr size_t kCounterBytes = kCounterTiles * 4;
 
-// Grows `s` to hold `payload` bytes after the counters and returns the payload's address.
+// Size of a grown buffer: at least twice the old one, so that the buffers a context retires
+// over its life add up to less than its largest one.
+size_t grown_size(size_t old_bytes, size_t need) { return std::max(need, 2 * old_bytes); }
+
+// Grows `s` to hold `payload` bytes after the counters and returns the payload's address. The
+// replaced buffer is retired, not freed: launches captured in a HIP graph keep its address.
 jv_status scratch_reserve(jv_scratch *s, size_t payload, void **out) {
     const size_t need = kCounterBytes + payload;
     if (s->bytes < need) {
-        if (s->buf) JV_HIP(hipFree(s->buf));
-        s->buf = nullptr;
-        s->bytes = 0;
-        JV_HIP(hipMalloc(&s->buf, need));
-        JV_HIP(hipMemset(s->buf, 0, kCounterBytes));
-        JV_HIP(hipDeviceSynchronize());
-        s->bytes = need;
+        const size_t size = grown_size(s->bytes, need);
+        void *buf = nullptr;
+        JV_HIP(hipMalloc(&buf, size));
+        hipError_t e = hipMemset(buf, 0, kCounterBytes);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) {
+            hipFree(buf);
+            return fail(JV_ERR_HIP, "scratch counters: %s", hipGetErrorString(e));
+        }
+        if (s->buf) s->retired.push_back(s->buf);
+        s->buf = buf;
+        s->bytes = size;
     }
     *out = (uint8_t *)s->buf + kCounterBytes;
     return JV_OK;
@@ -450,11 +464,13 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     const int mtiles = jobs_or_tiles * (int)(plan.bm / 16);
     const size_t need = (size_t)mtiles * 16 * w->k * 2;
     if (ctx->pack_bytes < need) {
-        if (ctx->pack) JV_HIP(hipFree(ctx->pack));
-        ctx->pack = nullptr;
-        ctx->pack_bytes = 0;
-        JV_HIP(hipMalloc(&ctx->pack, need));
-        ctx->pack_bytes = need;
+        // the smaller buffer is retired, not freed (graphs captured on it keep its address)
+        const size_t size = grown_size(ctx->pack_bytes, need);
+        void *buf = nullptr;
+        JV_HIP(hipMalloc(&buf, size));
+        if (ctx->pack) ctx->retired.push_back(ctx->pack);
+        ctx->pack = buf;
+        ctx->pack_bytes = size;
     }
     PackXParams pk{};
     pk.x = x;
@@ -715,6 +731,7 @@ void jv_close(jv_ctx *ctx) {
     if (!ctx) return;
     hipSetDevice(ctx->device);
     if (ctx->pack) hipFree(ctx->pack);
+    for (void *b : ctx->retired) hipFree(b);
     jv_scratch_free(ctx->own);
     if (ctx->module) hipModuleUnload(ctx->module);
     delete ctx;
@@ -951,9 +968,10 @@ jv_status jv_scratch_new(jv_ctx *ctx, jv_scratch **out) {
 
 void jv_scratch_free(jv_scratch *s) {
     if (!s) return;
-    if (s->buf) {
+    if (s->buf || !s->retired.empty()) {
         hipSetDevice(s->ctx->device);
-        hipFree(s->buf);
+        if (s->buf) hipFree(s->buf);
+        for (void *b : s->retired) hipFree(b);
     }
     delete s;
 }
