@@ -133,6 +133,22 @@ void jv_scratch_free(jv_scratch *s);
 jv_status jv_matmul(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
                     const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
                     jv_scratch *scratch, void *stream);
+/* Bytes of the fixed device array of jv_matmul_noalloc, one per GPU: 256 KiB of split-K tile
+ * counters, then the staging payload. */
+#define JV_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* No counterpart in the reference. For callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. The product and its
+ * kernels are jv_matmul's with a scratch buffer, but every staging buffer (packed activations of
+ * the tiled products, split-K partials and tile counters) lives in one fixed device array of
+ * JV_NOALLOC_SCRATCH_BYTES per GPU, set up by jv_open. The call allocates and frees no memory.
+ * A product that needs more staging than the array holds is rejected with JV_ERR_INVALID (the
+ * message names the bytes needed and the limit). All calls on one GPU share that GPU's array,
+ * which keeps the last call's contents: calls that overlap on one GPU (on other streams, or from
+ * other contexts or threads) race. */
+jv_status jv_matmul_noalloc(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                            const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
+                            void *stream);
 /* Product with an explicit plan (matmul_plan, gemm.rs:1093-1119). Plans with splits == 1 are
  * row invariant: every output row is accumulated in the same order whatever m or the tile. */
 jv_status jv_matmul_plan(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,

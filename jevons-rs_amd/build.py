@@ -2,7 +2,9 @@
 
 Outputs (git-ignored, shipped with the tree):
   jevons-rs_amd/lib/jevons_qmm.hsaco    kernels, loaded at run time with hipModuleLoad
-  jevons-rs_amd/lib/libjevons_qmm.so    C ABI of include/jevons_qmm.h
+  jevons-rs_amd/lib/libjevons_qmm.so    C ABI of include/jevons_qmm.h (host code, plus the
+                                        fixed device array of jv_matmul_noalloc in its own
+                                        gfx950 code object)
 
 Run as a script (``python jevons-rs_amd/build.py``) or call ``build()``.
 """
@@ -23,6 +25,8 @@ KERNEL_SRC = os.path.join(HERE, "csrc", "kernels", "qmm.hip")
 HOST_SRC = os.path.join(HERE, "csrc", "host", "jevons_qmm.cpp")
 TUNE_SRC = os.path.join(HERE, "csrc", "host", "tune.cpp")
 GGUF_SRC = os.path.join(HERE, "csrc", "host", "gguf.cpp")
+NOALLOC_SRC = os.path.join(HERE, "csrc", "host", "noalloc.hip")
+NOALLOC_OBJ = os.path.join(LIB_DIR, "noalloc.o")
 
 # Packed FP32 VALU instructions are disabled for all device code.
 HIPCC_FLAGS = [
@@ -36,20 +40,26 @@ def kernel_cmd(out: str = HSACO) -> list[str]:
     return [os.path.join(ROCM, "bin", "hipcc"), *HIPCC_FLAGS, "-c", KERNEL_SRC, "-o", out]
 
 
+def noalloc_cmd(out: str = NOALLOC_OBJ) -> list[str]:
+    """Host object holding a device array (host and device passes of hipcc)."""
+    return [os.path.join(ROCM, "bin", "hipcc"), "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC",
+            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+            "-I", os.path.join(ROOT, "include"), "-c", NOALLOC_SRC, "-o", out]
+
+
 def host_cmd(out: str = SO) -> list[str]:
     return [
         "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
         "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROOT, "include"),
-        "-I", os.path.join(ROCM, "include"), HOST_SRC, TUNE_SRC, GGUF_SRC,
+        "-I", os.path.join(ROCM, "include"), HOST_SRC, TUNE_SRC, GGUF_SRC, NOALLOC_OBJ,
         "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
         "-o", out,
     ]
 
 
-def build(verbose: bool = False) -> None:
-    os.makedirs(LIB_DIR, exist_ok=True)
-    # Build into temporaries and rename, so a failed build never leaves a half-written file.
-    jobs = [(kernel_cmd(HSACO + ".tmp"), HSACO), (host_cmd(SO + ".tmp"), SO)]
+def _run_all(jobs, verbose: bool) -> None:
+    """Runs (command, output) jobs in parallel; each writes output + ".tmp", renamed on success,
+    so a failed build never leaves a half-written file."""
     procs = []
     for cmd, _ in jobs:
         if verbose:
@@ -69,6 +79,12 @@ def build(verbose: bool = False) -> None:
     if failed:
         msg = "\n\n".join(" ".join(c) + "\n" + o for c, o in failed)
         raise RuntimeError("build failed:\n" + msg)
+
+
+def build(verbose: bool = False) -> None:
+    os.makedirs(LIB_DIR, exist_ok=True)
+    _run_all([(kernel_cmd(HSACO + ".tmp"), HSACO), (noalloc_cmd(NOALLOC_OBJ + ".tmp"), NOALLOC_OBJ)], verbose)
+    _run_all([(host_cmd(SO + ".tmp"), SO)], verbose)
 
 
 if __name__ == "__main__":

@@ -23,6 +23,11 @@
 
 #include "../qmm_params.h"
 
+// Fixed device array of jv_matmul_noalloc (noalloc.hip): set-up on the current device, and the
+// address kept for a device.
+extern "C" hipError_t jv_internal_noalloc_setup(int device, size_t zero_bytes, void **out);
+extern "C" void *jv_internal_noalloc_ptr(int device, hipError_t *status);
+
 namespace {
 
 thread_local std::string g_error;
@@ -162,6 +167,7 @@ struct jv_scratch {
     void *buf = nullptr;
     size_t bytes = 0;
     std::vector<void *> retired;  // smaller buffers kept for graphs captured on them
+    bool fixed = false;  // the fixed array of jv_matmul_noalloc: never grows, never freed here
 };
 
 namespace {
@@ -179,6 +185,11 @@ size_t grown_size(size_t old_bytes, size_t need) { return std::max(need, 2 * old
 // replaced buffer is retired, not freed: launches captured in a HIP graph keep its address.
 jv_status scratch_reserve(jv_scratch *s, size_t payload, void **out) {
     const size_t need = kCounterBytes + payload;
+    if (s->fixed && s->bytes < need)
+        return fail(JV_ERR_INVALID,
+                    "the product needs %zu bytes of staging; the fixed scratch array holds %zu "
+                    "(JV_NOALLOC_SCRATCH_BYTES, %zu of them tile counters)",
+                    payload, s->bytes - kCounterBytes, kCounterBytes);
     if (s->bytes < need) {
         const size_t size = grown_size(s->bytes, need);
         void *buf = nullptr;
@@ -456,14 +467,20 @@ bool pipelined_plan(const jv_qmatrix *w, jv_plan plan) {
             (plan.bm == 64 && plan.bn == 64) || (reg_format(w) && plan.bm == 32 && plan.bn == 64));
 }
 
+// `fixed` (the array of jv_matmul_noalloc, or null) holds the packed activations in place of the
+// context's own buffer.
 jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, const jv_qmatrix *w,
                            void *out, jv_out out_type, jv_plan plan, void *stream,
-                           const GroupArgs *grp) {
+                           const GroupArgs *grp, jv_scratch *fixed = nullptr) {
     jv_status st = JV_OK;
     const int jobs_or_tiles = grp ? (int)grp->max_jobs : (int)((m + plan.bm - 1) / plan.bm);
     const int mtiles = jobs_or_tiles * (int)(plan.bm / 16);
     const size_t need = (size_t)mtiles * 16 * w->k * 2;
-    if (ctx->pack_bytes < need) {
+    void *pack = ctx->pack;
+    if (fixed) {
+        st = scratch_reserve(fixed, need, &pack);
+        if (st != JV_OK) return st;
+    } else if (ctx->pack_bytes < need) {
         // the smaller buffer is retired, not freed (graphs captured on it keep its address)
         const size_t size = grown_size(ctx->pack_bytes, need);
         void *buf = nullptr;
@@ -471,10 +488,11 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
         if (ctx->pack) ctx->retired.push_back(ctx->pack);
         ctx->pack = buf;
         ctx->pack_bytes = size;
+        pack = buf;
     }
     PackXParams pk{};
     pk.x = x;
-    pk.out = (uint16_t *)ctx->pack;
+    pk.out = (uint16_t *)pack;
     pk.M = (int32_t)m;
     pk.K = (int32_t)w->k;
     pk.ldx = (int32_t)w->k;
@@ -493,7 +511,7 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     st = launch(ctx, "jv_pack_x", dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, pargs);
     if (st != JV_OK) return st;
     GemmParams gp{};
-    gp.xa = (const uint16_t *)ctx->pack;
+    gp.xa = (const uint16_t *)pack;
     gp.wq = w->q;
     gp.wh = w->h;
     gp.wd = w->d;
@@ -648,7 +666,9 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
             return launch(ctx, name, dim3((unsigned)((T + tw - 1) / tw)), dim3(64 * waves), lds, stream, args);
         }
     }
-    if (pipelined_plan(w, plan)) return launch_pipelined(ctx, x, act, m, w, out, out_type, plan, stream, nullptr);
+    if (pipelined_plan(w, plan))
+        return launch_pipelined(ctx, x, act, m, w, out, out_type, plan, stream, nullptr,
+                                scratch && scratch->fixed ? scratch : nullptr);
     return launch_tiles(ctx, x, act, m, w, out, out_type, scratch, plan, stream, nullptr);
 }
 
@@ -723,6 +743,10 @@ jv_status jv_open(int device, jv_ctx **out) {
     ctx->info.lds_bytes = prop.sharedMemPerBlock;
     ctx->info.total_memory = prop.totalGlobalMem;
     snprintf(ctx->info.arch, sizeof ctx->info.arch, "%.63s", prop.gcnArchName);
+    // The fixed array of jv_matmul_noalloc: its device address on this device, its tile counters
+    // zeroed. A failure here is reported by jv_matmul_noalloc; the other entry points do not use it.
+    void *fixed_ptr = nullptr;
+    (void)jv_internal_noalloc_setup(device, kCounterBytes, &fixed_ptr);
     *out = ctx;
     return JV_OK;
 }
@@ -982,6 +1006,27 @@ jv_status jv_matmul(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t
     if (!w) return fail(JV_ERR_INVALID, "null weight matrix");
     return run_product(ctx, x, act, x_len, m, w, out, out_type, out_len,
                        jv_plan_auto(w, m, 0), scratch, stream);
+}
+
+jv_status jv_matmul_noalloc(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                            const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
+                            void *stream) {
+    if (!ctx) return fail(JV_ERR_INVALID, "null context");
+    if (!w) return fail(JV_ERR_INVALID, "null weight matrix");
+    hipError_t e = hipSuccess;
+    void *ptr = jv_internal_noalloc_ptr(ctx->device, &e);
+    if (!ptr)
+        return fail(JV_ERR_HIP, "the fixed scratch array is not set up on device %d: %s", ctx->device,
+                    hipGetErrorString(e));
+    // jv_matmul with a scratch buffer that is the fixed array: same plan, kernels and bits; the
+    // buffer never grows (a product needing more is rejected before any launch)
+    jv_scratch fixed;
+    fixed.ctx = ctx;
+    fixed.buf = ptr;
+    fixed.bytes = JV_NOALLOC_SCRATCH_BYTES;
+    fixed.fixed = true;
+    return run_product(ctx, x, act, x_len, m, w, out, out_type, out_len, jv_plan_auto(w, m, 0), &fixed,
+                       stream);
 }
 
 jv_status jv_matmul_plan(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,

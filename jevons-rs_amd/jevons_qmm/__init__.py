@@ -84,6 +84,7 @@ def lib() -> C.CDLL:
         "jv_scratch_new": (I, [P, PP]),
         "jv_scratch_free": (None, [P]),
         "jv_matmul": (I, [P, P, I, S, S, P, P, I, S, P, P]),
+        "jv_matmul_noalloc": (I, [P, P, I, S, S, P, P, I, S, P]),
         "jv_matmul_plan": (I, [P, P, I, S, S, P, P, I, S, P, jv_plan, P]),
         "jv_matvec": (I, [P, P, I, S, S, P, P, I, S, P]),
         "jv_matmul_split": (I, [P, P, I, S, S, P, P, I, S, U32, U32, U32, P, P]),
@@ -314,6 +315,16 @@ def matmul(gpu: Gpu, x, m: int, w: QMatrix, out, scratch: SplitScratch | None = 
     """out[m, n] = x[m, k] . W^T with this library's gfx950 plan (gemm.rs:1069-1088)."""
     _check(lib().jv_matmul(gpu.handle, _dev(x), _act(x), x.numel(), m, w.handle, _dev(out),
                            _out(out), out.numel(), _sh(scratch), _stream(stream)))
+
+
+def matmul_noalloc(gpu: Gpu, x, m: int, w: QMatrix, out, stream=None):
+    """matmul's product staged through the library's fixed device array instead of allocated
+    buffers (no counterpart in the reference; for callers that cannot allocate)."""
+    _check(lib().jv_matmul_noalloc(gpu.handle, _dev(x), _act(x), x.numel(), m, w.handle, _dev(out),
+                                   _out(out), out.numel(), _stream(stream)))
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20  # JV_NOALLOC_SCRATCH_BYTES
 
 
 def matmul_plan(gpu: Gpu, x, m: int, w: QMatrix, out, scratch: SplitScratch | None, plan: Plan,

@@ -1,0 +1,66 @@
+"""The allocation-free product (jv_matmul_noalloc) against jv_matmul with an allocated scratch
+buffer: the same bits on every kernel family that stages through the fixed device array (packed
+activations of the tiled products, split-K partials of the generic tiles, split-K small-row
+partials and tile counters), on consecutive calls whose inputs shrink, and a clear rejection of a
+product whose staging exceeds the array."""
+import numpy as np
+import pytest
+import torch
+
+import jevons_qmm as jq
+from helpers import activations, say
+from jevons_qmm import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    yield jq.Gpu(0)
+
+
+def _upload(gpu, kind, n, k, seed):
+    return jq.QMatrix.upload(gpu, kind, n, k, 1, synth.weights(kind, seed, n, k))
+
+
+def _compare(gpu, w, kind, n, k, m, seed):
+    x, _ = activations("bf16", synth.normal_rows(seed, m, k))
+    want = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    got = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    jq.matmul(gpu, x, m, w, want, jq.SplitScratch(gpu))
+    jq.matmul_noalloc(gpu, x, m, w, got)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), (kind, n, k, m)
+
+
+def test_noalloc_equals_matmul_on_shrinking_inputs(gpu):
+    q4 = _upload(gpu, jq.Q4K, 2048, 3840, 1)
+    q6 = _upload(gpu, jq.Q6K, 1024, 15360, 2)
+    # (matrix, m): the 64 x 64 / 256 x 128 pipelined tiles (packed activations in the array),
+    # generic tiles with split-K (partials), persistent and per-tile small-row kernels (no
+    # staging), and the split-K small-row kernel of a long K (partials and tile counters)
+    calls = [(q4, jq.Q4K, 2048, 3840, 256), (q4, jq.Q4K, 2048, 3840, 64), (q4, jq.Q4K, 2048, 3840, 40),
+             (q6, jq.Q6K, 1024, 15360, 8), (q6, jq.Q6K, 1024, 15360, 4), (q4, jq.Q4K, 2048, 3840, 3),
+             (q4, jq.Q4K, 2048, 3840, 1)]
+    for i, (w, kind, n, k, m) in enumerate(calls):
+        say("noalloc", kind, n, k, m)
+        _compare(gpu, w, kind, n, k, m, 100 + i)
+    # the same product twice in a row, the second smaller, after a larger product of another matrix
+    for m in (200, 17):
+        say("noalloc again", m)
+        _compare(gpu, q4, jq.Q4K, 2048, 3840, m, 300 + m)
+
+
+def test_noalloc_rejects_staging_beyond_the_array(gpu):
+    n, k, m = 2048, 3840, 8192  # packed activations: 8192 x 3840 x 2 B = 60 MiB > 32 MiB
+    w = _upload(gpu, jq.Q4K, n, k, 3)
+    x = torch.zeros((m, k), dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    with pytest.raises(jq.JvError) as e:
+        jq.matmul_noalloc(gpu, x, m, w, out)
+    assert "fixed scratch array" in str(e.value)
+    assert str(m * k * 2) in str(e.value)
+    # nothing ran: the output is untouched, and the entry point still works afterwards
+    torch.cuda.synchronize()
+    assert not out.any()
+    _compare(gpu, w, jq.Q4K, n, k, 64, 7)
