@@ -88,6 +88,60 @@ def graph_of(fn, count):
 GEMV_N, GEMV_K, GEMV_MS = 15360, 3840, (1, 4, 8)
 
 
+class StreamProbe:
+    """The code object's memory floor probe (jv_probe_stream_read), launched through the HIP
+    module API: one launch reads `nbytes` with 16-byte loads, `per` bytes per workgroup."""
+
+    def __init__(self):
+        import ctypes as C
+
+        import jevons_qmm as jq
+
+        self.C = C
+        self.hip = C.CDLL("libamdhip64.so")
+        self.mod, self.fn = C.c_void_p(), C.c_void_p()
+        self._ok(self.hip.hipModuleLoad(C.byref(self.mod), jq.HSACO_PATH.encode()))
+        self._ok(self.hip.hipModuleGetFunction(C.byref(self.fn), self.mod, b"jv_probe_stream_read"))
+
+    @staticmethod
+    def _ok(e):
+        if e != 0:
+            raise RuntimeError(f"HIP error {e}")
+
+    def launch(self, src, nbytes, per, sink):
+        import torch
+
+        C = self.C
+        units = nbytes // 16
+        per_u = per // 16
+        grid = (units + per_u - 1) // per_u
+        a_src, a_units, a_per, a_sink = (C.c_void_p(src.data_ptr()), C.c_int64(units), C.c_int32(per_u),
+                                         C.c_void_p(sink.data_ptr()))
+        args = (C.c_void_p * 4)(*[C.cast(C.pointer(a), C.c_void_p) for a in (a_src, a_units, a_per, a_sink)])
+        stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        self._ok(self.hip.hipModuleLaunchKernel(self.fn, grid, 1, 1, 512, 1, 1, 0, stream, args, None))
+
+
+def stream_floor(nbytes, copies, reps):
+    """Average duration (us) of one streaming read of `nbytes`, each launch on the next of
+    `copies` buffers (the products' weight rotation), for several bytes per workgroup."""
+    import torch
+
+    probe = StreamProbe()
+    bufs = [torch.full((nbytes,), i, dtype=torch.uint8, device="cuda") for i in range(copies)]
+    sink = torch.zeros(nbytes // 16, dtype=torch.int32, device="cuda")
+    res = {}
+    # one Q4_K tile (16 rows x 15 blocks, the M=1 kernel's workgroup), half and twice that, and
+    # one range per compute unit
+    for per in (17280, 34560, 69120, (nbytes + 255) // 256 // 16 * 16 + 16):
+        probe.launch(bufs[0], nbytes, per, sink)
+        torch.cuda.synchronize()
+        t = kernel_time_ms(lambda r, per=per: probe.launch(bufs[r % copies], nbytes, per, sink), reps)
+        res[str(per)] = round(t * 1e3, 3)
+    del bufs
+    return res
+
+
 def pmc_child():
     """Launch workload of the traffic passes: each GEMV launch 20 times on rotating weight copies,
     then a device copy of the weight byte count 20 times."""
@@ -240,12 +294,12 @@ def measure_configs(gpu, steps):
     # Q8_0 GEMV
     n, k = 4096, 4096
     ms, wbytes = mats(jq.Q8_0, n, k, max(2, math.ceil(ROTATION_BYTES / (n * k // 32 * 34))), 3)
-    x = xrows(1, k, 1)
+    x = torch.from_numpy(synth.normal_rows(1, 1, k)).cuda()  # f32 activations, as the config states
     out = torch.empty((1, n), dtype=torch.float32, device="cuda")
     jq.matmul(gpu, x, 1, ms[0], out, scratch)  # buffers grow outside graph capture
     t = kernel_time_ms(lambda r: jq.matmul(gpu, x, 1, ms[r % len(ms)], out, scratch), steps)
     gbs = wbytes / (t * 1e-3) / 1e9
-    res["q8_0_gemv"] = {"workload": f"Q8_0 GEMV M=1 K={k} N={n}, bf16 activations, f32 out",
+    res["q8_0_gemv"] = {"workload": f"Q8_0 GEMV M=1 K={k} N={n}, f32 activations, f32 out",
                         "kernel_us": round(t * 1e3, 3), "weight_bytes": wbytes,
                         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
@@ -272,8 +326,23 @@ def measure_configs(gpu, steps):
         fsum += flops
         del ms
     tf = fsum / (tsum * 1e-3) / 1e12
+    # the q, k and v projections as one Q4_K product [8192, 3840] on their shared input
+    n, k = 4096 + 2 * 2048, 3840
+    ms, _ = mats(jq.Q4K, n, k, 2, 5)
+    x = xrows(m, k, 2)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    plan = jq.Plan.auto(ms[0], m, row_invariant=True)
+    jq.matmul_plan(gpu, x, m, ms[0], out, scratch, plan)
+    t = kernel_time_ms(lambda r: jq.matmul_plan(gpu, x, m, ms[r % 2], out, scratch, plan), max(4, steps // 4))
+    fflops = 2.0 * m * n * k
+    fused = {"n": n, "k": k, "format": "Q4_K", "plan": [plan.bm, plan.bn, plan.splits], "us": round(t * 1e3, 2),
+             "tflops": round(fflops / (t * 1e-3) / 1e12, 1),
+             "separate_qkv_us": round(sum(per[nm]["us"] for nm in ("q", "k", "v")), 2)}
+    del ms
     res["layer_gemms_m256"] = {"workload": "one transformer block's six GEMMs at M=256, bf16 activations, f32 out",
-                               "gemms": per, "total_us": round(tsum * 1e3, 2),
+                               "gemms": per, "fused_qkv": fused, "total_us": round(tsum * 1e3, 2),
+                               "total_us_fused_qkv": round((tsum - sum(per[nm]["us"] for nm in ("q", "k", "v")) * 1e-3
+                                                            + t) * 1e3, 2),
                                "roofline": {"bound": "mfma", "achieved": round(tf, 1),
                                             "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                             "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}}
@@ -468,6 +537,8 @@ def main():
     avg_kernel_ms = sum(kt) / len(kt)
     achieved = wbytes / (avg_kernel_ms * 1e-3) / 1e9
     log("gemv per M:", per_m)
+    floor = stream_floor(wbytes, copies, reps)
+    log("stream floor (us by bytes per workgroup):", floor)
 
     # prefill GEMM, M = 512
     mg = 512
@@ -540,6 +611,9 @@ def main():
             "weight_bytes_per_launch": wbytes,
             "rotation_copies": copies,
             "per_m": per_m,
+            # plain 16-byte streaming read of the same bytes and rotation, by bytes per workgroup
+            "stream_floor_us": min(floor.values()),
+            "stream_floor_by_workgroup_bytes": floor,
         },
         "roofline": {
             "bound": "hbm",

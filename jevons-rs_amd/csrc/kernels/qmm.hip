@@ -2417,3 +2417,29 @@ extern "C" __global__ __launch_bounds__(256) void jv_argmax_final(const float *p
     }
     if (threadIdx.x == 0) index[row] = (sbad[0] || chunks == 0) ? -1 : si[0];
 }
+
+// ---------------------------------------------------------------------------------------------
+// Memory floor probe (benchmark only, not a product kernel): workgroup b reads the 16-byte units
+// [b per, (b + 1) per) of src, each thread its units t, t + 512, ... with eight loads in flight,
+// and folds them into one word. The word is stored only if it equals a value that the
+// benchmark's inputs do not produce, so the loads cannot be dropped; sink holds one word per
+// workgroup. Its duration is the time one launch takes to stream the same bytes as a product.
+// ---------------------------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(512) void jv_probe_stream_read(const uint4 *src, int64_t units,
+                                                                       int32_t per, uint32_t *sink) {
+    const int64_t base = (int64_t)blockIdx.x * per;
+    const int64_t end = min(base + (int64_t)per, units);
+    uint32_t acc = 0;
+    constexpr int kInFlight = 8;
+    for (int64_t i0 = base + threadIdx.x; i0 < end; i0 += kInFlight * 512) {
+        uint4 v[kInFlight];
+#pragma unroll
+        for (int j = 0; j < kInFlight; ++j) {
+            const int64_t i = i0 + (int64_t)j * 512;
+            v[j] = i < end ? src[i] : uint4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int j = 0; j < kInFlight; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    }
+    if (acc == 0x8badf00du) sink[blockIdx.x] = acc;
+}
