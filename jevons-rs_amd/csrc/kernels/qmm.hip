@@ -2349,50 +2349,91 @@ __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
     }
 }
 
-// Grid (chunks, rows): partial (max, index) of logits[row][c*chunk, min(n, (c+1)*chunk)).
-extern "C" __global__ __launch_bounds__(256) void jv_argmax_partial(const float *logits, int64_t n,
-                                                                    int chunk, float *pval,
-                                                                    int *pidx) {
-    __shared__ float sv[256];
-    __shared__ int si[256];
-    __shared__ int sbad[256];
-    const int row = blockIdx.y;
-    const int c = blockIdx.x;
-    const int64_t lo = (int64_t)c * chunk;
-    const int64_t hi = min(n, lo + chunk);
-    const float *x = logits + (int64_t)row * n;
-    float bv = -__builtin_inff();
-    int bi = 0x7fffffff;
-    int bad = 0;
-    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
-        const float v = x[i];
-        if (!__builtin_isfinite(v)) bad = 1;
-        better(bv, bi, v, (int)i);
-    }
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
-    sbad[threadIdx.x] = bad;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w) {
-            better(sv[threadIdx.x], si[threadIdx.x], sv[threadIdx.x + w], si[threadIdx.x + w]);
-            sbad[threadIdx.x] |= sbad[threadIdx.x + w];
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) {
-        const int64_t o = (int64_t)row * gridDim.x + c;
-        pval[o] = sv[0];
-        pidx[o] = sbad[0] ? -1 : si[0];
+// (max, index) of a wave's lanes under better(); every lane ends with the result.
+__device__ __forceinline__ void wave_best(float &v, int &i) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(v, off);
+        const int oi = __shfl_xor(i, off);
+        better(v, i, ov, oi);
     }
 }
 
-// Grid (rows): combine the partials of each row.
+// (max, index) of a 256-thread workgroup; thread 0 holds the result. `bad` is or-ed the same way.
+__device__ __forceinline__ void group_best(float &v, int &i, int &bad) {
+    __shared__ float sv[4];
+    __shared__ int si[4], sb[4];
+    wave_best(v, i);
+    bad = __any(bad) ? 1 : 0;
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[wave] = v;
+        si[wave] = i;
+        sb[wave] = bad;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) {
+            better(v, i, sv[w], si[w]);
+            bad |= sb[w];
+        }
+    }
+}
+
+// Grid (chunks, rows), 256 threads: partial (max, index) of logits[row][c chunk, min(n, (c + 1)
+// chunk)), index -1 when that range holds a non-finite value (greedy's error,
+// crates/jevons-core/src/model.rs:207-219). `vec` (rows 16-byte aligned, chunk a multiple of
+// 1024): each thread loads chunk / 1024 float4 at once; otherwise scalar loads.
+extern "C" __global__ __launch_bounds__(256) void jv_argmax_partial(const float *logits, int64_t n,
+                                                                   int chunk, int vec, float *pval,
+                                                                   int *pidx) {
+    const int row = blockIdx.y;
+    const int64_t c0 = (int64_t)blockIdx.x * chunk;
+    const int64_t c1 = min(c0 + (int64_t)chunk, n);
+    const float *src = logits + (int64_t)row * n;
+    float bv = -__builtin_inff();
+    int bi = 0x7fffffff;
+    int bad = 0;
+    if (vec) {
+        constexpr int kMaxLoads = 4;  // chunk <= 4096
+        const int loads = chunk >> 10;
+        float4 v[kMaxLoads];
+#pragma unroll
+        for (int j = 0; j < kMaxLoads; ++j) {
+            const int64_t e = c0 + 4 * ((int64_t)j * 256 + threadIdx.x);
+            if (j < loads && e < c1) v[j] = *(const float4 *)(src + e);
+        }
+#pragma unroll
+        for (int j = 0; j < kMaxLoads; ++j) {
+            const int64_t e = c0 + 4 * ((int64_t)j * 256 + threadIdx.x);
+            if (j < loads && e < c1) {
+                const float x[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    bad |= !__builtin_isfinite(x[q]);
+                    better(bv, bi, x[q], (int)(e + q));
+                }
+            }
+        }
+    } else {
+        for (int64_t e = c0 + threadIdx.x; e < c1; e += 256) {
+            const float x = src[e];
+            bad |= !__builtin_isfinite(x);
+            better(bv, bi, x, (int)e);
+        }
+    }
+    group_best(bv, bi, bad);
+    if (threadIdx.x == 0) {
+        const int64_t o = (int64_t)row * gridDim.x + blockIdx.x;
+        pval[o] = bv;
+        pidx[o] = bad ? -1 : bi;
+    }
+}
+
+// Grid (rows), 256 threads: combine the partials of each row; -1 if any range was non-finite or
+// the row is empty.
 extern "C" __global__ __launch_bounds__(256) void jv_argmax_final(const float *pval, const int *pidx,
                                                                   int chunks, int *index) {
-    __shared__ float sv[256];
-    __shared__ int si[256];
-    __shared__ int sbad[256];
     const int row = blockIdx.x;
     float bv = -__builtin_inff();
     int bi = 0x7fffffff;
@@ -2404,18 +2445,8 @@ extern "C" __global__ __launch_bounds__(256) void jv_argmax_final(const float *p
         else
             better(bv, bi, pval[(int64_t)row * chunks + c], i);
     }
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
-    sbad[threadIdx.x] = bad;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w) {
-            better(sv[threadIdx.x], si[threadIdx.x], sv[threadIdx.x + w], si[threadIdx.x + w]);
-            sbad[threadIdx.x] |= sbad[threadIdx.x + w];
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) index[row] = (sbad[0] || chunks == 0) ? -1 : si[0];
+    group_best(bv, bi, bad);
+    if (threadIdx.x == 0) index[row] = (bad || chunks == 0) ? -1 : bi;
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -712,6 +712,35 @@ def test_argmax_follows_greedy(gpu):
     assert jq.argmax_rows(gpu, empty, s).cpu().tolist() == [-1, -1, -1]
 
 
+def _greedy_or_minus_one(row):
+    try:
+        return O.greedy(row)[0]
+    except O.OracleError:  # non-finite logits (model.rs:212-214)
+        return -1
+
+
+@pytest.mark.parametrize("n", [1, 3, 5, 1023, 1024, 4097, 65536, 262144])
+def test_argmax_random_rows_with_ties(gpu, n):
+    """Rows drawn from a few integer values (many ties, first maximum wins), some rows holding a
+    NaN or an infinity, on 16-byte aligned rows (vector loads when n % 4 == 0) and on rows that
+    start one float past an aligned address (scalar loads), against greedy."""
+    s = jq.SplitScratch(gpu)
+    rng = np.random.default_rng(n)
+    rows = 9
+    host = rng.integers(-3, 4, size=(rows, n)).astype(np.float32)
+    host[1, rng.integers(0, n)] = np.nan
+    host[2, rng.integers(0, n)] = np.inf
+    host[3, rng.integers(0, n)] = -np.inf
+    host[4] = -5.0  # one value everywhere: index 0
+    want = [_greedy_or_minus_one(r) for r in host]
+    aligned = torch.from_numpy(host).cuda()
+    assert jq.argmax_rows(gpu, aligned, s).cpu().tolist() == want
+    buf = torch.empty(rows * n + 1, dtype=torch.float32, device="cuda")
+    buf[1:] = aligned.reshape(-1)
+    shifted = buf[1:].view(rows, n)
+    assert jq.argmax_rows(gpu, shifted, s).cpu().tolist() == want
+
+
 @pytest.mark.parametrize("m", [1, 8, 32])
 def test_q6k_lm_head_logits_and_argmax(gpu, m):
     """Q6_K vocabulary projection K=3840 on 16384 rows of the vocabulary: logits against the f64
