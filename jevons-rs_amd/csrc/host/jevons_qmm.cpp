@@ -384,6 +384,76 @@ struct GroupArgs {
     uint32_t cap;
 };
 
+// Staging buffers of one product: `pack_bytes` of packed or converted activations (the context's
+// buffer, grown as needed) and `part_bytes` of split-K partials (after the counters of
+// `scratch`). With the fixed array of jv_matmul_noalloc both come from that array, one after
+// the other, and nothing is allocated.
+jv_status stage_buffers(jv_ctx *ctx, jv_scratch *scratch, size_t pack_bytes, size_t part_bytes,
+                        void **pack, void **part) {
+    *pack = nullptr;
+    *part = nullptr;
+    if (scratch && scratch->fixed) {
+        const size_t at = align_up(pack_bytes, 256);
+        void *payload = nullptr;
+        jv_status st = scratch_reserve(scratch, at + part_bytes, &payload);
+        if (st != JV_OK) return st;
+        if (pack_bytes) *pack = payload;
+        if (part_bytes) *part = (uint8_t *)payload + at;
+        return JV_OK;
+    }
+    if (pack_bytes && ctx->pack_bytes < pack_bytes) {
+        // the smaller buffer is retired, not freed (graphs captured on it keep its address)
+        const size_t size = grown_size(ctx->pack_bytes, pack_bytes);
+        void *buf = nullptr;
+        JV_HIP(hipMalloc(&buf, size));
+        if (ctx->pack) ctx->retired.push_back(ctx->pack);
+        ctx->pack = buf;
+        ctx->pack_bytes = size;
+    }
+    if (pack_bytes) *pack = ctx->pack;
+    if (part_bytes) {
+        if (!scratch) return fail(JV_ERR_INVALID, "split-K plans need a scratch buffer");
+        return scratch_reserve(scratch, part_bytes, part);
+    }
+    return JV_OK;
+}
+
+// jv_pack_x: `rows` rows of x into FP16 MFMA fragments (mtiles 16-row tiles; grouped: per
+// job, rows_cap rows each) or, with `rowmajor` (BF16 and FP32 only), into FP16 rows [rows][K];
+// rscale receives every packed row's range factor.
+jv_status launch_pack(jv_ctx *ctx, const void *x, jv_act act, size_t rows, size_t k, int mtiles,
+                      int rowmajor, uint16_t *out, float *rscale, const GroupArgs *grp, uint32_t rows_cap,
+                      void *stream) {
+    PackXParams pk{};
+    pk.x = x;
+    pk.out = out;
+    pk.rscale = rscale;
+    pk.M = (int32_t)rows;
+    pk.K = (int32_t)k;
+    pk.ldx = (int32_t)k;
+    pk.act = (int32_t)act;
+    pk.mtiles = mtiles;
+    pk.rowmajor = rowmajor;
+    if (grp) {
+        pk.ids = grp->ids;
+        pk.offsets = grp->offsets;
+        pk.jobs = grp->jobs;
+        pk.grouped = 1;
+        pk.in_div = (int32_t)grp->in_div;
+        pk.rows_cap = (int32_t)rows_cap;
+    }
+    void *args[] = {&pk};
+    if (act == JV_ACT_F16) {  // a copy thread per 128 values of a packed row
+        const size_t waves = (size_t)mtiles * (k / 256) * 2;
+        return launch(ctx, "jv_pack_x", dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, args);
+    }
+    // a workgroup per 4 rows, 4 NW waves (NW = min(4, ceil(K / 2048))): at most 8 chunks per thread
+    const size_t packed_rows = rowmajor ? rows : (size_t)mtiles * 16;
+    const size_t nw = std::min<size_t>(4, (k + 2047) / 2048);
+    return launch(ctx, "jv_pack_x", dim3((unsigned)((packed_rows + 3) / 4)), dim3((unsigned)(256 * nw)), 0,
+                  stream, args);
+}
+
 // The generic tile kernel (any plan, split-K through the scratch buffer and jv_reduce_splits).
 // m = output rows; grouped launches cover grp->max_jobs jobs of at most grp->cap rows.
 jv_status launch_tiles(jv_ctx *ctx, const void *x, jv_act act, size_t m, const jv_qmatrix *w,
@@ -406,8 +476,24 @@ jv_status launch_tiles(jv_ctx *ctx, const void *x, jv_act act, size_t m, const j
         return fail(JV_ERR_INVALID, "tile needs %zu bytes of LDS, the device has %zu", lds,
                     ctx->info.lds_bytes);
 
+    // BF16 and FP32 rows are converted once into FP16 rows divided by their range factors
+    // (jv_pack_x, row-major): the kernel stages FP16 and multiplies each output row by
+    // its input row's factor.
+    const size_t in_rows = grp ? (m + grp->in_div - 1) / grp->in_div : m;
+    const size_t conv_bytes = act == JV_ACT_F16 ? 0 : align_up(in_rows * w->k * 2, 256) + in_rows * 4;
+    void *conv = nullptr, *partials = nullptr;
+    st = stage_buffers(ctx, scratch, conv_bytes, splits > 1 ? (size_t)splits * m * w->n * 4 : 0, &conv,
+                       &partials);
+    if (st != JV_OK) return st;
+    float *rscale = nullptr;
+    if (conv) {
+        rscale = (float *)((uint8_t *)conv + align_up(in_rows * w->k * 2, 256));
+        st = launch_pack(ctx, x, act, in_rows, w->k, 0, 1, (uint16_t *)conv, rscale, nullptr, 0, stream);
+        if (st != JV_OK) return st;
+    }
+
     QmmParams p{};
-    p.x = x;
+    p.x = conv ? conv : x;
     p.wq = w->q;
     p.wh = w->h;
     p.wd = w->d;
@@ -416,8 +502,9 @@ jv_status launch_tiles(jv_ctx *ctx, const void *x, jv_act act, size_t m, const j
     p.K = (int32_t)w->k;
     p.ldx = (int32_t)w->k;
     p.ldo = (int32_t)w->n;
-    p.act = (int32_t)act;
+    p.act = (int32_t)JV_ACT_F16;
     p.out_type = (int32_t)out_type;
+    p.rscale = rscale;
     p.kc = kc;
     p.splits = splits;
     p.split_stride = (int64_t)(m * w->n);
@@ -429,15 +516,7 @@ jv_status launch_tiles(jv_ctx *ctx, const void *x, jv_act act, size_t m, const j
         p.in_div = (int32_t)grp->in_div;
         p.rows_cap = (int32_t)grp->cap;
     }
-    if (splits > 1) {
-        if (!scratch) return fail(JV_ERR_INVALID, "split-K plans need a scratch buffer");
-        void *partials = nullptr;
-        st = scratch_reserve(scratch, (size_t)splits * m * w->n * 4, &partials);
-        if (st != JV_OK) return st;
-        p.out = partials;
-    } else {
-        p.out = out;
-    }
+    p.out = splits > 1 ? partials : out;
     char name[64];
     snprintf(name, sizeof name, "jv_qmm_%s_m%d_n%d", fmt_kernel_name(w->fmt), MT, NT);
     const size_t gy = grp ? grp->max_jobs : (m + 16 * MT - 1) / (16 * MT);
@@ -475,43 +554,17 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     jv_status st = JV_OK;
     const int jobs_or_tiles = grp ? (int)grp->max_jobs : (int)((m + plan.bm - 1) / plan.bm);
     const int mtiles = jobs_or_tiles * (int)(plan.bm / 16);
-    const size_t need = (size_t)mtiles * 16 * w->k * 2;
-    void *pack = ctx->pack;
-    if (fixed) {
-        st = scratch_reserve(fixed, need, &pack);
-        if (st != JV_OK) return st;
-    } else if (ctx->pack_bytes < need) {
-        // the smaller buffer is retired, not freed (graphs captured on it keep its address)
-        const size_t size = grown_size(ctx->pack_bytes, need);
-        void *buf = nullptr;
-        JV_HIP(hipMalloc(&buf, size));
-        if (ctx->pack) ctx->retired.push_back(ctx->pack);
-        ctx->pack = buf;
-        ctx->pack_bytes = size;
-        pack = buf;
-    }
-    PackXParams pk{};
-    pk.x = x;
-    pk.out = (uint16_t *)pack;
-    pk.M = (int32_t)m;
-    pk.K = (int32_t)w->k;
-    pk.ldx = (int32_t)w->k;
-    pk.act = (int32_t)act;
-    pk.mtiles = mtiles;
-    if (grp) {
-        pk.ids = grp->ids;
-        pk.offsets = grp->offsets;
-        pk.jobs = grp->jobs;
-        pk.grouped = 1;
-        pk.in_div = (int32_t)grp->in_div;
-        pk.rows_cap = (int32_t)plan.bm;
-    }
-    const int64_t threads = (int64_t)mtiles * (int64_t)(w->k / 256) * 2 * 64;
-    void *pargs[] = {&pk};
-    st = launch(ctx, "jv_pack_x", dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, pargs);
+    // fragments, then each packed row's range factor
+    const size_t frag_bytes = (size_t)mtiles * 16 * w->k * 2;
+    void *pack = nullptr, *none = nullptr;
+    st = stage_buffers(ctx, fixed, frag_bytes + (size_t)mtiles * 16 * 4, 0, &pack, &none);
+    if (st != JV_OK) return st;
+    float *rscale = (float *)((uint8_t *)pack + frag_bytes);
+    st = launch_pack(ctx, x, act, m, w->k, mtiles, 0, (uint16_t *)pack, rscale, grp, plan.bm, stream);
     if (st != JV_OK) return st;
     GemmParams gp{};
     gp.xa = (const uint16_t *)pack;
+    gp.rscale = rscale;
     gp.wq = w->q;
     gp.wh = w->h;
     gp.wd = w->d;
@@ -585,13 +638,14 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         const int T = (int)(w->n / 16);
         const int umax = (U + waves - 1) / waves;
         const int tw = q6 || m <= 2 ? 1 : 2;  // tiles per workgroup of the per-tile kernels
-        // per wave: FP16 activations [m][ku umax + 8], sums [m][ku umax / xg] and, for Q6_K, a
-        // zero row [ku umax + 8]. The per-tile kernels reuse it for the wave's tile partials
-        // (tw KB); the persistent ones add two chunks of 2 tiles x waves partials; the split-K
-        // ones share one such region per workgroup. The kernels compute the same sizes.
+        // per wave: FP16 activations [m][ku umax + 8], sums [m][ku umax / xg], for Q6_K a zero
+        // row [ku umax + 8], and m range factors. The per-tile kernels reuse it for the wave's
+        // tile partials (tw KB); the persistent ones add two chunks of 2 tiles x waves partials;
+        // the split-K ones share one such region per workgroup, plus a flag per wave. The kernels
+        // compute the same sizes.
         const size_t row = ((size_t)umax * ku + 8) * 2;
-        const size_t stage = ((size_t)m * row + (size_t)m * umax * (ku / xg) * 4 + (q6 ? row : 0) + 15) &
-                             ~(size_t)15;
+        const size_t stage = ((size_t)m * row + (size_t)m * umax * (ku / xg) * 4 + (q6 ? row : 0) +
+                              (size_t)m * 4 + 15) & ~(size_t)15;
         const size_t lmax = ctx->info.lds_bytes;
         const size_t lds_persist = stage * waves + 2 * 2 * (size_t)waves * 1024;
         const size_t lds_tile = std::max(stage, (size_t)tw * 1024) * waves;
@@ -608,14 +662,14 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         const bool fsplit = force && force[0] == '1', fnosplit = force && force[0] == '0';
         // A product given no scratch buffer (jv_matvec) whose only fitting small-row kernel is
         // split-K uses the context's own, so that its rows keep the bits of every other m.
-        if (!scratch && lds_tile > lmax && !(wide && lds_persist <= lmax) && stage <= lmax) {
+        if (!scratch && lds_tile > lmax && !(wide && lds_persist <= lmax) && stage + 64 <= lmax) {
             if (!ctx->own) {
                 ctx->own = new jv_scratch();
                 ctx->own->ctx = ctx;
             }
             scratch = ctx->own;
         }
-        const bool split_ok = scratch && U >= waves && (size_t)T <= kCounterTiles && stage <= lmax;
+        const bool split_ok = scratch && U >= waves && (size_t)T <= kCounterTiles && stage + 64 <= lmax;
         // Persistent workgroups stage the activations once for several tiles: they serve wide
         // matrices and, above 2 rows, any matrix (at m = 4-8 on the decode shapes 10-34% faster
         // than the per-tile kernels, whose staging per tile or tile pair dominates there).
@@ -650,7 +704,8 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
                 const int groups = (T + waves - 1) / waves;
                 const int gp = (groups + 7) & ~7;  // the kernel's XCD mapping pads groups to 8
                 snprintf(name, sizeof name, "jv_qmvs_%s_m%d", fname, mv);
-                return launch(ctx, name, dim3((unsigned)(waves * gp)), dim3(64 * waves), stage, stream, args);
+                return launch(ctx, name, dim3((unsigned)(waves * gp)), dim3(64 * waves), stage + 64, stream,
+                              args);
             }
             if (persist) {
                 snprintf(name, sizeof name, "jv_qmvp_%s_m%d", fname, mv);
@@ -1141,10 +1196,11 @@ jv_status jv_matvec_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len
         const int U = (int)(w->k / ku);
         const int umax = (U + waves - 1) / waves;
         // per wave, as the kernel computes it: FP16 activations [mv][ku umax + 8], sums
-        // [mv][ku umax / xg], a zero row for Q6_K; at least the 1 KB of the tile partial
+        // [mv][ku umax / xg], a zero row for Q6_K, mv range factors; at least the 1 KB of the
+        // tile partial
         const size_t mv = mr == 1 ? 1 : 2;  // rows per chunk
         const size_t row = ((size_t)umax * ku + 8) * 2;
-        const size_t stage = (mv * row + mv * umax * (ku / xg) * 4 + (q6 ? row : 0) + 15) & ~(size_t)15;
+        const size_t stage = (mv * row + mv * umax * (ku / xg) * 4 + (q6 ? row : 0) + mv * 4 + 15) & ~(size_t)15;
         const size_t lds = std::max(stage, (size_t)1024) * waves;
         if (lds <= ctx->info.lds_bytes) {
             QmmParams p{};

@@ -393,8 +393,9 @@ __device__ __forceinline__ f16x8 frag_f16(const typename F::Raw &r, const typena
 }
 
 // ---------------------------------------------------------------------------------------------
-// Activation staging: rows [m0, m0 + rows) x k [k0, k0 + kl) -> LDS FP16, row stride `stride`
-// (grouped: sorted positions m0 .. m0 + rows, each reading input row ids[s] / in_div).
+// Activation staging: FP16 rows [m0, m0 + rows) x k [k0, k0 + kl) -> LDS, row stride `stride`
+// (grouped: sorted positions m0 .. m0 + rows, each reading input row ids[s] / in_div). BF16 and
+// FP32 rows reach the generic kernel as FP16 rows prescaled by jv_pack_x (rowmajor).
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ void stage_rows(const QmmParams &p, _Float16 *lds, int m0, int rows,
                                            int k0, int kl, int stride) {
@@ -405,24 +406,7 @@ __device__ __forceinline__ void stage_rows(const QmmParams &p, _Float16 *lds, in
         const int c8 = i - r * per_row;
         const int xr = p.grouped ? (int)(p.ids[m0 + r] / (uint32_t)p.in_div) : m0 + r;
         const size_t src = (size_t)xr * (size_t)p.ldx + (size_t)(k0 + 8 * c8);
-        f16x8 v;
-        if (p.act == 0) {
-            v = __builtin_bit_cast(f16x8, *(const uint4 *)((const uint16_t *)p.x + src));
-        } else if (p.act == 1) {
-            const uint4 b = *(const uint4 *)((const uint16_t *)p.x + src);
-            const uint32_t w[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[2 * e] = (_Float16)bf2f(w[e]);
-                v[2 * e + 1] = (_Float16)bf2f(w[e] >> 16);
-            }
-        } else {
-            const float4 a = *(const float4 *)((const float *)p.x + src);
-            const float4 b = *(const float4 *)((const float *)p.x + src + 4);
-            v[0] = (_Float16)a.x; v[1] = (_Float16)a.y; v[2] = (_Float16)a.z; v[3] = (_Float16)a.w;
-            v[4] = (_Float16)b.x; v[5] = (_Float16)b.y; v[6] = (_Float16)b.z; v[7] = (_Float16)b.w;
-        }
-        *(f16x8 *)(lds + r * stride + 8 * c8) = v;
+        *(uint4 *)(lds + r * stride + 8 * c8) = *(const uint4 *)((const uint16_t *)p.x + src);
     }
 }
 
@@ -518,10 +502,12 @@ __device__ __forceinline__ void qmm_body(const QmmParams &p) {
             const int lr = mt * 16 + 4 * g + i;
             if (lr >= rows_real) continue;
             const int row = p.grouped ? (int)p.ids[m0 + lr] : m0 + lr;
+            // the input row's range factor (prescaled FP16 rows; exact, a power of two)
+            const float rs = p.rscale ? p.rscale[p.grouped ? row / p.in_div : row] : 1.f;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const int col = n_base + 16 * t + r16;
-                const float v = acc[mt][t][i];
+                const float v = acc[mt][t][i] * rs;
                 if (p.splits > 1) {
                     float *o = (float *)p.out + (int64_t)z * p.split_stride;
                     o[(size_t)row * (size_t)p.ldo + (size_t)col] = v;
@@ -632,8 +618,10 @@ __device__ __forceinline__ uint4 q4k_head_gather(uint32_t hv) {
 // xs[r * stride + c] and FP32 sums of each XG-column group (16 or 32) into Xs[r * xstride + c / XG].
 // The wave's first XB 16-byte loads per lane are issued before `after()` (the weight loads),
 // so waiting for them does not wait for the weights; later batches, if any, come after.
+// Returns true in a lane that wrote a non-finite sum: some staged value of that sub-block was
+// non-finite, which for finite BF16 and FP32 inputs means it overflowed the FP16 range.
 template <int ACT, int XB, int XG, bool GRP = false, class After>
-__device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int ncols, _Float16 *xs,
+__device__ __forceinline__ bool stage_wave_cols(const QmmParams &p, int c0, int ncols, _Float16 *xs,
                                                 int stride, float *Xs, int xstride, int lane,
                                                 After after) {
     constexpr int EPL = ACT == 2 ? 4 : 8;  // elements per 16-byte load
@@ -644,7 +632,7 @@ __device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int 
     // chunk i = row r, 8-column group c8: r = floor((i + 0.5) / per_row) through a float
     // reciprocal, exact for i < 2^22 (the rounding error stays below the 0.5 / per_row margin)
     const float rcp = 1.0f / (float)per_row;
-    bool issued = false;
+    bool issued = false, nonfinite = false;
     for (int i0 = 0; i0 < total; i0 += XC * 64) {
         uint4 raw[XC][LPC];
         int rq[XC], cq[XC];
@@ -712,16 +700,18 @@ __device__ __forceinline__ void stage_wave_cols(const QmmParams &p, int c0, int 
             part += __shfl_xor(part, 1);
             if (XG == 32) part += __shfl_xor(part, 2);
             if (i < total && (c8 & (XG / 8 - 1)) == 0) Xs[r * xstride + c8 / (XG / 8)] = part;
+            nonfinite |= !__builtin_isfinite(part);
         }
     }
     if (!issued) after();
+    return nonfinite;
 }
 
 // stage_wave_cols with the work shared by the W waves of a workgroup: the 8-element chunks are
 // numbered row-major and wave w takes the 64-chunk batches w, w + W, w + 2W, ... Each chunk's
 // values and sums are computed as in stage_wave_cols.
 template <int ACT, int XB, int XG, int W, class After>
-__device__ __forceinline__ void stage_group_cols(const QmmParams &p, int c0, int ncols, _Float16 *xs,
+__device__ __forceinline__ bool stage_group_cols(const QmmParams &p, int c0, int ncols, _Float16 *xs,
                                                  int stride, float *Xs, int xstride, int lane,
                                                  int wave, After after) {
     constexpr int EPL = ACT == 2 ? 4 : 8;  // elements per 16-byte load
@@ -732,7 +722,7 @@ __device__ __forceinline__ void stage_group_cols(const QmmParams &p, int c0, int
     // chunk i = row r, 8-column group c8: r = floor((i + 0.5) / per_row) through a float
     // reciprocal, exact for i < 2^22 (the rounding error stays below the 0.5 / per_row margin)
     const float rcp = 1.0f / (float)per_row;
-    bool issued = false;
+    bool issued = false, nonfinite = false;
     for (int i0 = 64 * wave; i0 < total; i0 += XC * 64 * W) {
         uint4 raw[XC][LPC];
         int rq[XC], cq[XC];
@@ -797,9 +787,112 @@ __device__ __forceinline__ void stage_group_cols(const QmmParams &p, int c0, int
             part += __shfl_xor(part, 1);
             if (XG == 32) part += __shfl_xor(part, 2);
             if (i < total && (c8 & (XG / 8 - 1)) == 0) Xs[r * xstride + c8 / (XG / 8)] = part;
+            nonfinite |= !__builtin_isfinite(part);
         }
     }
     if (!issued) after();
+    return nonfinite;
+}
+
+// Power-of-two range scale of a row whose largest magnitude is `mx` (the reference's
+// F16_ROW_LIMIT rule, crates/jevons-burn/src/kernels.rs:105, :120-130, with a power of two, so
+// that the scaling is exact): 2^-e with e = floor(log2 mx) - 13 when mx > 16384, so that the
+// scaled magnitudes stay below 2^14; 1 for smaller or non-finite maxima (a non-finite value
+// stays non-finite in the product, as in the reference). Returns 2^-e and sets *inv = 2^e.
+__device__ __forceinline__ float range_scale(float mx, float *inv) {
+    if (!(mx > 16384.f) || !__builtin_isfinite(mx)) {
+        *inv = 1.f;
+        return 1.f;
+    }
+    const int e = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xffu) - 127 - 13;  // 1..114
+    *inv = __builtin_bit_cast(float, (uint32_t)(127 + e) << 23);
+    return __builtin_bit_cast(float, (uint32_t)(127 - e) << 23);
+}
+
+// The 8 activations of chunk (row xr, columns col .. col + 7) as FP32.
+template <int ACT>
+__device__ __forceinline__ void load_act8(const QmmParams &p, int xr, int col, float v[8]) {
+    const size_t src = (size_t)xr * (size_t)p.ldx + (size_t)col;
+    if (ACT == 2) {
+        const float4 a = *(const float4 *)((const float *)p.x + src);
+        const float4 b = *(const float4 *)((const float *)p.x + src + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        const uint4 b = *(const uint4 *)((const uint16_t *)p.x + src);
+        const uint32_t w[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = ACT == 0 ? h2f(w[e]) : bf2f(w[e]);
+            v[2 * e + 1] = ACT == 0 ? h2f(w[e] >> 16) : bf2f(w[e] >> 16);
+        }
+    }
+}
+
+// Stages row r of columns [c0, c0 + ncols) again, as stage_wave_cols does, but multiplied by the
+// row's range_scale over those columns; one wave. Sc[r] receives the factor that undoes it. Runs
+// only when a staged value overflowed the FP16 range (rows without values above 16384 get scale
+// 1 and so the same values as the first staging).
+template <int ACT, int XG, bool GRP>
+__device__ __forceinline__ void stage_row_scaled(const QmmParams &p, int r, int c0, int ncols,
+                                                 _Float16 *xs, int stride, float *Xs, int xstride,
+                                                 float *Sc, int lane) {
+    const int per_row = ncols >> 3;  // a multiple of 4
+    const int xr = GRP ? (int)(p.ids[r] / (uint32_t)p.in_div) : r;
+    float mx = 0.f;
+    bool nf = false;
+    for (int c = lane; c < per_row; c += 64) {
+        float v[8];
+        load_act8<ACT>(p, xr, c0 + 8 * c, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            nf |= !__builtin_isfinite(v[e]);
+            mx = __builtin_fmaxf(mx, __builtin_fabsf(v[e]));
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off));
+    float inv;
+    const float scale = range_scale(__any(nf) ? __builtin_inff() : mx, &inv);
+    if (lane == 0) Sc[r] = inv;
+    for (int c00 = 0; c00 < per_row; c00 += 64) {  // uniform trip count: the sums shuffle
+        const int c = c00 + lane;
+        float part = 0.f;
+        if (c < per_row) {
+            float v[8];
+            load_act8<ACT>(p, xr, c0 + 8 * c, v);
+            f16x8 h;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = (_Float16)(v[e] * scale);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                part = __builtin_amdgcn_fdot2(f16x2{h[2 * e], h[2 * e + 1]}, f16x2{1.0f16, 1.0f16}, part, false);
+            *(f16x8 *)(xs + r * stride + 8 * c) = h;
+        }
+        part += __shfl_xor(part, 1);
+        if (XG == 32) part += __shfl_xor(part, 2);
+        if (c < per_row && (c & (XG / 8 - 1)) == 0) Xs[r * xstride + c / (XG / 8)] = part;
+    }
+}
+
+// A wave's staging of its columns for all p.M rows (stage_wave_cols), redone row by row with range
+// scales when some value overflowed FP16. Returns whether it was (wave-uniform); then Sc[r] holds
+// the factor that undoes row r's scale.
+template <int ACT, int XB, int XG, bool GRP, class After>
+__device__ __forceinline__ bool stage_wave_checked(const QmmParams &p, int c0, int ncols, _Float16 *xs,
+                                                   int stride, float *Xs, int xstride, float *Sc,
+                                                   int lane, After after) {
+    const bool nf = stage_wave_cols<ACT, XB, XG, GRP>(p, c0, ncols, xs, stride, Xs, xstride, lane, after);
+    if (!__any(nf)) return false;
+    for (int r = 0; r < p.M; ++r)
+        stage_row_scaled<ACT, XG, GRP>(p, r, c0, ncols, xs, stride, Xs, xstride, Sc, lane);
+    return true;
+}
+
+// Multiplies a lane's accumulator (output rows 4g .. 4g + 3) by the rows' range factors.
+__device__ __forceinline__ void unscale_rows(f32x4 &a, const float *Sc, int g, int M) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] *= Sc[min(4 * g + i, M - 1)];
 }
 
 // One block against activations staged in LDS, with the scale arithmetic regrouped to cut
@@ -1053,15 +1146,18 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p, int wt_off = 0) {
     const int umax = (U + W - 1) / W;
     const int stride = umax * G::KU + kLdsPad;
     const int xstride = umax * (G::KU / G::XG);
-    // per wave: FP16 activations [M][stride], sums [M][xstride], and for formats that mask
-    // activation fragments a zero row [stride]; reused for the partials
+    // per wave: FP16 activations [M][stride], sums [M][xstride], for formats that mask
+    // activation fragments a zero row [stride], and the rows' range factors [M]; reused for the
+    // partials
     const int zbytes = G::kZeroRow ? stride * 2 : 0;
-    const int region = max((p.M * stride * 2 + p.M * xstride * 4 + zbytes + 15) & ~15, TW * 1024);  // bytes
+    const int region = max((p.M * stride * 2 + p.M * xstride * 4 + zbytes + p.M * 4 + 15) & ~15, TW * 1024);
     uint8_t *mine = (uint8_t *)lds + (size_t)wave * region;
     _Float16 *xs = (_Float16 *)mine;
     float *Xs = (float *)(mine + p.M * stride * 2);
     _Float16 *zrow = (_Float16 *)(mine + p.M * stride * 2 + p.M * xstride * 4);
+    float *Sc = (float *)(mine + p.M * stride * 2 + p.M * xstride * 4 + zbytes);
     const int nitems = nu * ntw;
+    bool scaled = false;  // wave-uniform: this wave's rows carry range factors
 
     auto load_item = [&](typename G::Item &dst, int idx) {
         idx = min(idx, nitems - 1);
@@ -1080,12 +1176,12 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p, int wt_off = 0) {
         const int c0 = u0 * G::KU, nc = nu * G::KU;
         if (G::kZeroRow)
             for (int i = lane; i < stride / 8; i += 64) *(f16x8 *)(zrow + 8 * i) = f16x8{};
-        if (p.act == 0)
+        if (p.act == 0)  // FP16 rows are in range by construction
             stage_wave_cols<0, XB, G::XG, GRP>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
         else if (p.act == 1)
-            stage_wave_cols<1, XB, G::XG, GRP>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
+            scaled = stage_wave_checked<1, XB, G::XG, GRP>(p, c0, nc, xs, stride, Xs, xstride, Sc, lane, issue);
         else
-            stage_wave_cols<2, XB, G::XG, GRP>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
+            scaled = stage_wave_checked<2, XB, G::XG, GRP>(p, c0, nc, xs, stride, Xs, xstride, Sc, lane, issue);
         // LDS operations of one wave complete in order; this keeps the compiler from moving
         // the fragment reads above the staging writes.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1112,6 +1208,10 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p, int wt_off = 0) {
                 if (i0 + P < nitems) load_item(buf[j], idx + P);
             }
         }
+    }
+    if (scaled) {  // before the partials overwrite the factors
+#pragma unroll
+        for (int t = 0; t < TW; ++t) unscale_rows(acc[t], Sc, g, p.M);
     }
     // this wave's staging region is no longer read: it takes the partials
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1165,12 +1265,14 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
     const int stride = umax * G::KU + kLdsPad;
     const int xstride = umax * (G::KU / G::XG);
     const int zbytes = G::kZeroRow ? stride * 2 : 0;
-    const int region = (p.M * stride * 2 + p.M * xstride * 4 + zbytes + 15) & ~15;  // bytes
+    const int region = (p.M * stride * 2 + p.M * xstride * 4 + zbytes + p.M * 4 + 15) & ~15;  // bytes
     uint8_t *mine = (uint8_t *)lds + (size_t)wave * region;
     _Float16 *xs = (_Float16 *)mine;
     float *Xs = (float *)(mine + p.M * stride * 2);
     _Float16 *zrow = (_Float16 *)(mine + p.M * stride * 2 + p.M * xstride * 4);
+    float *Sc = (float *)(mine + p.M * stride * 2 + p.M * xstride * 4 + zbytes);  // range factors
     f32x4 *part = (f32x4 *)((uint8_t *)lds + (size_t)W * region);  // [2][TS][W][64]
+    bool scaled = false;  // wave-uniform: this wave's rows carry range factors
 
     int chunk = 0, tt = 0;
     auto store = [&](int tile, const f32x4 &v) {
@@ -1190,7 +1292,9 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
     // this wave's partial of tile tt of the current chunk is `a`
     auto end_tile = [&](const f32x4 &a) {
         const int tc = min(TS, nt - chunk * TS);
-        part[(((chunk & 1) * TS + tt) * W + wave) * 64 + lane] = a;
+        f32x4 v = a;
+        if (scaled) unscale_rows(v, Sc, g, p.M);
+        part[(((chunk & 1) * TS + tt) * W + wave) * 64 + lane] = v;
         if (++tt == tc) {
             lds_barrier();
             for (int t = wave; t < tc; t += W) {
@@ -1229,9 +1333,9 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
         if (p.act == 0)
             stage_wave_cols<0, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
         else if (p.act == 1)
-            stage_wave_cols<1, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
+            scaled = stage_wave_checked<1, XB, G::XG, false>(p, c0, nc, xs, stride, Xs, xstride, Sc, lane, issue);
         else
-            stage_wave_cols<2, XB, G::XG>(p, c0, nc, xs, stride, Xs, xstride, lane, issue);
+            scaled = stage_wave_checked<2, XB, G::XG, false>(p, c0, nc, xs, stride, Xs, xstride, Sc, lane, issue);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
         const int arow = min(r16, p.M - 1);  // rows >= M feed output rows that are never stored
@@ -1291,6 +1395,10 @@ __device__ __forceinline__ void qmvs_body(const QmmParams &p) {
     _Float16 *xs = (_Float16 *)lds;
     float *Xs = (float *)((uint8_t *)lds + p.M * stride * 2);
     _Float16 *zrow = (_Float16 *)((uint8_t *)lds + p.M * stride * 2 + p.M * xstride * 4);
+    const int zbytes = G::kZeroRow ? stride * 2 : 0;
+    float *Sc = (float *)((uint8_t *)lds + p.M * stride * 2 + p.M * xstride * 4 + zbytes);  // range factors
+    int *wflag = (int *)(Sc + p.M);  // [W]: a wave's staging overflowed FP16
+    bool scaled = false;             // workgroup-uniform
     const int tile = tg * W + wave;
     const bool live = tile < T;  // wave-uniform
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1308,14 +1416,27 @@ __device__ __forceinline__ void qmvs_body(const QmmParams &p) {
         const int c0 = u0 * G::KU, nc = nu * G::KU;
         if (G::kZeroRow)
             for (int i = (int)threadIdx.x; i < stride / 8; i += 64 * W) *(f16x8 *)(zrow + 8 * i) = f16x8{};
+        bool nf = false;
         if (p.act == 0)
             stage_group_cols<0, XB, G::XG, W>(p, c0, nc, xs, stride, Xs, xstride, lane, wave, issue);
         else if (p.act == 1)
-            stage_group_cols<1, XB, G::XG, W>(p, c0, nc, xs, stride, Xs, xstride, lane, wave, issue);
+            nf = stage_group_cols<1, XB, G::XG, W>(p, c0, nc, xs, stride, Xs, xstride, lane, wave, issue);
         else
-            stage_group_cols<2, XB, G::XG, W>(p, c0, nc, xs, stride, Xs, xstride, lane, wave, issue);
+            nf = stage_group_cols<2, XB, G::XG, W>(p, c0, nc, xs, stride, Xs, xstride, lane, wave, issue);
+        if (lane == 0) wflag[wave] = __any(nf) ? 1 : 0;
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         lds_barrier();
+        for (int w = 0; w < W; ++w) scaled |= wflag[w] != 0;
+        if (scaled) {  // some value overflowed FP16: the waves stage the slice again, row by row
+            for (int r = wave; r < p.M; r += W) {
+                if (p.act == 1)
+                    stage_row_scaled<1, G::XG, false>(p, r, c0, nc, xs, stride, Xs, xstride, Sc, lane);
+                else
+                    stage_row_scaled<2, G::XG, false>(p, r, c0, nc, xs, stride, Xs, xstride, Sc, lane);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            lds_barrier();
+        }
         if (live) {
             const int arow = min(r16, p.M - 1);  // rows >= M feed output rows that are never stored
             const _Float16 *xrow = xs + arow * stride;
@@ -1337,6 +1458,7 @@ __device__ __forceinline__ void qmvs_body(const QmmParams &p) {
     const int lg = ln >> 4;
     const int col = tile * 16 + (ln & 15);
     const size_t plane = (size_t)p.M * (size_t)p.N;
+    if (scaled) unscale_rows(acc, Sc, lg, p.M);
     // Partials are written and read at device scope (sc1: through to the level every compute
     // unit sees, no cache-wide write-back or invalidate); the store acknowledgements are awaited
     // before the count, and the reads are issued only after the count completes.
@@ -1539,13 +1661,155 @@ extern "C" __global__ __launch_bounds__(256) void jv_reduce_splits(const float *
         ((uint16_t *)out)[i] = (uint16_t)f2bf(sum);
 }
 
+// The 8 values at x[row][col .. col + 7] as raw words (one 16-byte load, two for FP32) ...
+template <int ACT>
+__device__ __forceinline__ void act8_load(const void *x, size_t o, u32x4 r[2]) {
+    if (ACT == 2) {
+        r[0] = *(const u32x4 *)((const float *)x + o);
+        r[1] = *(const u32x4 *)((const float *)x + o + 4);
+    } else {
+        r[0] = *(const u32x4 *)((const uint16_t *)x + o);
+    }
+}
+// ... multiplied by s (the inverse of the row's range factor, a power of two: exact) and rounded
+// to nearest even into FP16; FP16 input is copied. Elements go through scalars (a bit cast of a
+// vector element directly is miscompiled).
+template <int ACT>
+__device__ __forceinline__ f16x8 act8_cvt(const u32x4 r[2], float s) {
+    if (ACT == 0) return __builtin_bit_cast(f16x8, r[0]);
+    f16x8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        uint32_t w;
+        if (ACT == 2) {
+            w = r[e >> 2][e & 3];
+        } else {
+            const uint32_t pair = r[0][e >> 1];
+            w = (pair >> (16 * (e & 1))) << 16;
+        }
+        h[e] = (_Float16)(__builtin_bit_cast(float, w) * s);
+    }
+    return h;
+}
+
 // ---------------------------------------------------------------------------------------------
-// Activation packing: rows -> FP16 MFMA A fragments (layout in qmm_params.h, PackXParams).
-// Conversions equal the staging of the tiled kernel: FP16 as is, BF16 and FP32 rounded to nearest
-// even. Thread ((mt * U + u) * 2 + half) * 64 + lane packs fragments s = 4 half .. 4 half + 3
-// of (mt, u), with four 16-byte loads in flight.
+// Activation packing: rows -> FP16 MFMA A fragments (layout in qmm_params.h, PackXParams), or
+// FP16 rows [M][K] (`rowmajor`, the generic tiled kernel's input).
+//  - FP16 rows are copied (pack_copy: thread ((mt * U + u) * 2 + half) * 64 + lane moves
+//    fragments s = 4 half .. 4 half + 3 of (mt, u), every store of a wave 1 KB contiguous).
+//  - BF16 and FP32 rows (pack_rows: one wave per row and its whole K) are divided by their range
+//    factor and rounded to nearest even. The factor is range_scale's: a power of two for rows
+//    whose largest magnitude exceeds 16384 (crates/jevons-burn/src/kernels.rs:105, :120-130),
+//    so the division is exact; 1 otherwise.
+// rscale[R] receives each packed (or row-major) row's factor, for the product to multiply its
+// outputs by; rows of padding pack zeros with factor 1, and unused job slots are skipped.
 // ---------------------------------------------------------------------------------------------
-extern "C" __global__ __launch_bounds__(256) void jv_pack_x(PackXParams p) {
+__device__ __forceinline__ uint16_t *frag_dst(const PackXParams &p, int R, int c) {
+    // chunk c (k = 8 c) of packed row R: fragment (mt U + u) 8 + s, lane 16 g + r
+    if (p.rowmajor) return p.out + (size_t)R * (size_t)p.K + 8 * (size_t)c;
+    const int U = p.K >> 8, mt = R >> 4, r16 = R & 15;
+    const int u = c >> 5, s = (c >> 2) & 7, g = c & 3;
+    return p.out + ((((size_t)mt * U + u) * 8 + s) * 64 + 16 * g + r16) * 8;
+}
+
+// Input row of packed row R (-1: padding or an unused row of a job; -2: an unused job slot).
+__device__ __forceinline__ int packed_source(const PackXParams &p, int R) {
+    if (!p.grouped) return R < p.M ? R : -1;
+    const int per = p.rows_cap >> 4;
+    const int job = (R >> 4) / per;
+    if (job >= (int)p.jobs[0]) return -2;
+    const int r = R - job * per * 16;
+    const uint32_t e = p.jobs[1 + 2 * job], s0 = p.jobs[2 + 2 * job];
+    return r < min((int)(p.offsets[e + 1] - s0), p.rows_cap) ? (int)(p.ids[s0 + r] / (uint32_t)p.in_div) : -1;
+}
+
+// BF16 / FP32 rows, 4 per workgroup of 4 NW waves: thread t handles row t % 4 and its chunks
+// t / 4 + 64 NW i (8 values each), so a wave's store writes 4 consecutive rows' 16-byte pieces
+// side by side (64 bytes) for 16 chunks. NW = min(4, ceil(K / 2048)) keeps each thread at 8
+// chunks or fewer, held in registers between the row's maximum and its conversion.
+template <int ACT>
+__device__ __forceinline__ void pack_rows(const PackXParams &p) {
+    __shared__ float wmax[16][4];
+    __shared__ int wnf[16][4];
+    const int nthreads = (int)blockDim.x;  // 256 NW
+    const int t = (int)threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int rr = t & 3, cl = t >> 2, tpr = nthreads >> 2;  // row of the group, chunk lane, per row
+    const int R = (int)blockIdx.x * 4 + rr;
+    const int rows_out = p.rowmajor ? p.M : p.mtiles * 16;
+    const int xr = R < rows_out ? packed_source(p, R) : -2;
+    const int chunks = p.K >> 3;
+    const size_t base = xr >= 0 ? (size_t)xr * (size_t)p.ldx : 0;
+    constexpr int B = 8;  // chunks held per thread
+    u32x4 r[B][2];
+    // Loads past the row's end read its last chunk again (unused): unguarded loads stay in flight
+    // together, where a branch around each would wait for the ones before it.
+    auto load_batch = [&](int c0) {
+#pragma unroll
+        for (int j = 0; j < B; ++j)
+            act8_load<ACT>(p.x, base + 8 * (size_t)min(c0 + tpr * j + cl, chunks - 1), r[j]);
+    };
+    float mx = 0.f;
+    bool nf = false;
+    const bool held = chunks <= tpr * B;  // one batch: the loads are kept for the conversion
+    if (xr >= 0) {
+        for (int c0 = 0; c0 < chunks; c0 += tpr * B) {
+            load_batch(c0);
+#pragma unroll
+            for (int j = 0; j < B; ++j) {
+                if (c0 + tpr * j + cl < chunks) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        uint32_t w;  // through a scalar: a bit cast of a vector element is miscompiled
+                        if (ACT == 2) {
+                            w = r[j][e >> 2][e & 3];
+                        } else {
+                            const uint32_t pair = r[j][0][e >> 1];
+                            w = (pair >> (16 * (e & 1))) << 16;
+                        }
+                        const float v = __builtin_bit_cast(float, w);
+                        nf |= !__builtin_isfinite(v);
+                        mx = __builtin_fmaxf(mx, __builtin_fabsf(v));
+                    }
+                }
+            }
+        }
+    }
+    // the row's maximum over the lanes of its row (same t % 4) and then over the waves
+    int inf = nf ? 1 : 0;
+#pragma unroll
+    for (int off = 4; off < 64; off <<= 1) {
+        mx = __builtin_fmaxf(mx, __shfl_xor(mx, off));
+        inf |= __shfl_xor(inf, off);
+    }
+    if (lane < 4) {
+        wmax[wave][rr] = mx;
+        wnf[wave][rr] = inf;
+    }
+    __syncthreads();
+    for (int w = 0; w < (nthreads >> 6); ++w) {
+        mx = __builtin_fmaxf(mx, wmax[w][rr]);
+        inf |= wnf[w][rr];
+    }
+    if (xr == -2) return;  // past the rows, or an unused job slot: nothing is read from it
+    float f;
+    const float s = range_scale(inf ? __builtin_inff() : mx, &f);
+    if (xr < 0) {
+        for (int c = cl; c < chunks; c += tpr) *(u32x4 *)frag_dst(p, R, c) = u32x4{0u, 0u, 0u, 0u};
+        if (cl == 0) p.rscale[R] = 1.f;
+        return;
+    }
+    for (int c0 = 0; c0 < chunks; c0 += tpr * B) {
+        if (!held) load_batch(c0);  // longer rows: read the batch again (from the cache)
+#pragma unroll
+        for (int j = 0; j < B; ++j) {
+            const int c = c0 + tpr * j + cl;
+            if (c < chunks) *(f16x8 *)frag_dst(p, R, c) = act8_cvt<ACT>(r[j], s);
+        }
+    }
+    if (cl == 0) p.rscale[R] = f;
+}
+
+__device__ __forceinline__ void pack_copy(const PackXParams &p) {
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int U = p.K >> 8;
     if (t >= (int64_t)p.mtiles * U * 2 * 64) return;
@@ -1553,63 +1817,32 @@ extern "C" __global__ __launch_bounds__(256) void jv_pack_x(PackXParams p) {
     const int64_t q = t >> 6;
     const int half = (int)(q & 1);
     const int64_t mu = q >> 1;
-    int row = (int)(mu / U) * 16 + (lane & 15);
-    bool live = row < p.M;
-    if (p.grouped) {  // m-tile mu / U is m-tile (mu / U) % per of job (mu / U) / per
-        const int per = p.rows_cap >> 4;
-        const int mtg = (int)(mu / U);
-        const int job = mtg / per;
-        const int r = (mtg - job * per) * 16 + (lane & 15);
-        if (job >= (int)p.jobs[0]) return;  // no product workgroup reads unused job slots
-        const uint32_t e = p.jobs[1 + 2 * job], s0 = p.jobs[2 + 2 * job];
-        live = r < min((int)(p.offsets[e + 1] - s0), p.rows_cap);
-        if (live) row = (int)(p.ids[s0 + r] / (uint32_t)p.in_div);
-    }
+    const int R = (int)(mu / U) * 16 + (lane & 15);  // packed row
+    const int row = packed_source(p, R);
+    if (row == -2) return;
     const int col0 = (int)(mu % U) * 256 + half * 128 + (lane >> 4) * 8;
     uint16_t *dst = p.out + ((mu * 8 + 4 * half) * 64 + lane) * 8;
-    f16x8 h[4];
-    if (live) {
-        const size_t o = (size_t)row * (size_t)p.ldx + (size_t)col0;
-        if (p.act == 0) {
-            uint4 w[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) w[s] = *(const uint4 *)((const uint16_t *)p.x + o + 32 * s);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) h[s] = __builtin_bit_cast(f16x8, w[s]);
-        } else if (p.act == 1) {
-            uint4 w[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) w[s] = *(const uint4 *)((const uint16_t *)p.x + o + 32 * s);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const uint32_t ww[4] = {w[s].x, w[s].y, w[s].z, w[s].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    h[s][2 * e] = (_Float16)bf2f(ww[e]);
-                    h[s][2 * e + 1] = (_Float16)bf2f(ww[e] >> 16);
-                }
-            }
-        } else {
-            float4 a[4], b[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                a[s] = *(const float4 *)((const float *)p.x + o + 32 * s);
-                b[s] = *(const float4 *)((const float *)p.x + o + 32 * s + 4);
-            }
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                h[s][0] = (_Float16)a[s].x; h[s][1] = (_Float16)a[s].y; h[s][2] = (_Float16)a[s].z; h[s][3] = (_Float16)a[s].w;
-                h[s][4] = (_Float16)b[s].x; h[s][5] = (_Float16)b[s].y; h[s][6] = (_Float16)b[s].z; h[s][7] = (_Float16)b[s].w;
-            }
-        }
-    } else {
+    u32x4 h[4] = {};
+    if (row >= 0) {
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) h[s][e] = (_Float16)0.f;
+            h[s] = *(const u32x4 *)((const uint16_t *)p.x + (size_t)row * (size_t)p.ldx + (size_t)(col0 + 32 * s));
     }
+    if (mu % U == 0 && half == 0 && lane < 16) p.rscale[R] = 1.f;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) *(f16x8 *)(dst + s * 512) = h[s];
+    for (int s = 0; s < 4; ++s) *(u32x4 *)(dst + s * 512) = h[s];
+}
+
+// Grid: FP16 fragments: mtiles * (K / 256) * 2 waves, 4 per workgroup; BF16 and FP32: one
+// workgroup of 4 NW waves per 4 packed rows (rowmajor: rows). FP16 rows never take the
+// row-major form.
+extern "C" __global__ __launch_bounds__(1024) void jv_pack_x(PackXParams p) {
+    if (p.act == 0)
+        pack_copy(p);
+    else if (p.act == 1)
+        pack_rows<1>(p);
+    else
+        pack_rows<2>(p);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1911,7 +2144,8 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
             const int col = (t0 + n_of(k)) * 16 + r;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                int m = (mt0 + m_of(i)) * 16 + 4 * g + e;
+                const int pr = (mt0 + m_of(i)) * 16 + 4 * g + e;  // packed row
+                int m = pr;
                 bool live = m < p.M;
                 if (p.grouped) {
                     const int ml = m_of(i) * 16 + 4 * g + e;  // row within the job
@@ -1920,10 +2154,11 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
                 }
                 if (live) {
                     const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
+                    const float v = acc[i][k][e] * p.rscale[pr];  // exact: a power of two
                     if (f32_out)
-                        ((float *)p.out)[o] = acc[i][k][e];
+                        ((float *)p.out)[o] = v;
                     else
-                        ((uint16_t *)p.out)[o] = (uint16_t)f2bf(acc[i][k][e]);
+                        ((uint16_t *)p.out)[o] = (uint16_t)f2bf(v);
                 }
             }
         }
@@ -2028,10 +2263,11 @@ __device__ __forceinline__ void gemm8_body(const GemmParams &p) {
             const int m = (mt0 + mq) * 16 + 4 * g + e;
             if (m < p.M) {
                 const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
+                const float v = acc[k][e] * p.rscale[m];  // exact: a power of two
                 if (f32_out)
-                    ((float *)p.out)[o] = acc[k][e];
+                    ((float *)p.out)[o] = v;
                 else
-                    ((uint16_t *)p.out)[o] = (uint16_t)f2bf(acc[k][e]);
+                    ((uint16_t *)p.out)[o] = (uint16_t)f2bf(v);
             }
         }
     }

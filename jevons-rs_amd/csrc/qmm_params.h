@@ -28,6 +28,9 @@ struct QmmParams {
     // 16-row tile (kept at a multiple of 16 between launches).
     float *part;
     uint32_t *counters;
+    // Tiled kernels: per input row, the factor that undoes the row's range scale (multiplied
+    // into its outputs); null for none. The activations were then prescaled FP16 rows.
+    const float *rscale;
 };
 
 // Decode probe: rows [row0, row0 + rows) of a weight matrix into [rows][K].
@@ -43,11 +46,16 @@ struct DequantParams {
 
 // Activation rows -> FP16 MFMA A fragments of 1 KB: fragment (mt * U + u) * 8 + s (U = K / 256)
 // holds, for lane 16g + r, x[16 mt + r][256 u + 32 s + 8 g + e], e < 8; rows >= M are zero.
+// Rows of BF16 or FP32 values above 16384 are divided by a power-of-two range factor first;
+// rscale[R] gets packed row R's factor, for the product to undo. With `rowmajor` (BF16 and
+// FP32 only, never grouped) the output is FP16 rows [M][K] and rscale per row.
 struct PackXParams {
     const void *x;       // [M][ldx] of `act`
-    uint16_t *out;       // FP16 bits, mtiles * (K / 32) fragments of 512 elements
+    uint16_t *out;       // FP16 bits, mtiles * (K / 32) fragments of 512 elements (or [M][K])
+    float *rscale;       // [mtiles * 16] (or [M])
     int32_t M, K, ldx, act;
     int32_t mtiles;      // 16-row tiles packed (M rounded up to the product's row tile)
+    int32_t rowmajor;
     // Expert-grouped mode: m-tiles [j rows_cap / 16, (j + 1) rows_cap / 16) hold job j's rows,
     // input rows ids[s] / in_div for sorted positions s of the job (QmmParams' job format).
     const uint32_t *ids, *offsets, *jobs;
@@ -61,6 +69,7 @@ struct GemmParams {
     const uint8_t *wh;
     const uint8_t *wd;
     void *out;           // [M][ldo] of `out_type`
+    const float *rscale; // per packed row, the factor undoing its range scale (jv_pack_x)
     int32_t M, N, K, ldo, out_type;
     // Expert-grouped mode (grid y = job): the job's rows come packed per job, its weight rows
     // start at expert * N, and its output rows are ids[start + r] (QmmParams' job format).

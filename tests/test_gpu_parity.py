@@ -968,3 +968,104 @@ def test_plan_rules_follow_the_reference(gpu):
     w4 = jq.QMatrix.upload(gpu, jq.Q4K, 256, 512, 1, synth.weights(jq.Q4K, 1, 256, 512))
     assert jq.Plan(256, 128, 1).valid_for(w4, 512)
     assert not jq.Plan(256, 128, 2).valid_for(w4, 512) and not jq.Plan(256, 64, 1).valid_for(w4, 512)
+
+
+# ------------------------------------------------------------------ activations beyond FP16
+
+def _wide_range_rows(seed, m, k, act):
+    """Rows of BF16 (or F32) values the FP16 staging cannot hold: a plain N(0,1) row; N(0,1)
+    x 1e-6 with a few +-1e6 spikes; N(0,1) with one value just above the FP16 maximum; N(0,1)
+    x 1e5 everywhere; (F32) 1e30 spikes on N(0,1). Rows repeat cyclically."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    kinds = 5 if act == "f32" else 4
+    for r in range(m):
+        kind = r % kinds
+        if kind == 1:
+            x[r] *= np.float32(1e-6)
+            cols = rng.choice(k, 5, replace=False)
+            x[r, cols] = rng.choice([-1e6, 1e6], 5).astype(np.float32)
+        elif kind == 2:
+            x[r, rng.integers(0, k)] = np.float32(70000.0)
+        elif kind == 3:
+            x[r] *= np.float32(1e5)
+        elif kind == 4:
+            x[r, rng.choice(k, 3, replace=False)] = np.float32(1e30)
+    return x
+
+
+def _row_errors(got, want):
+    got = np.asarray(got, np.float64)
+    return [float(np.max(np.abs(g - w)) / max(1e-300, np.max(np.abs(w)))) for g, w in zip(got, want)]
+
+
+@pytest.mark.parametrize("act", ["bf16", "f32"])
+@pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0)])
+def test_activations_beyond_the_fp16_range(gpu, monkeypatch, name, type_id, act):
+    """Rows whose values overflow FP16 (+-1e6 spikes over 1e-6 values, 7e4, 1e5-scale rows, 1e30 in
+    F32) through the small-row kernels (per-tile, persistent, split-K), the tiled plans
+    (pipelined and generic, with split-K) and the grouped products (pipelined and generic tiles,
+    small-row jobs of 1, 2 and 4 rows): every row within 1e-3 of its own largest f64 oracle
+    value. A row's power-of-two range scale is exact, so plain rows keep their bits: the small-row
+    products of the plain rows alone equal those rows of the mixed batch."""
+    n, k = 256, 2048
+    raw = synth.weights(type_id, 90, n, k)
+    w = jq.QMatrix.upload(gpu, type_id, n, k, 1, raw)
+    dense = O.dequantize(type_id, raw).reshape(n, k)
+    scratch = jq.SplitScratch(gpu)
+
+    def check(got, want, what):
+        errs = _row_errors(got, want)
+        assert max(errs) <= TOL, (what, np.argmax(errs), max(errs))
+
+    # small-row kernels
+    for m, env in ((1, {}), (4, {}), (4, {"JV_QMV_PERSIST": "0"}), (12, {}), (12, {"JV_QMV_SPLIT": "0"})):
+        for kk, v in env.items():
+            monkeypatch.setenv(kk, v)
+        x32 = _wide_range_rows(91 + m, m, k, act)
+        x, xv = activations(act, x32)
+        out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matmul(gpu, x, m, w, out, scratch)
+        got = out.cpu().numpy()
+        check(got, O.matmul_f64(xv, dense), ("small-row", m, env))
+        plain = [r for r in range(m) if r % (5 if act == "f32" else 4) == 0]
+        if len(plain) > 1:  # the plain rows alone: the same bits
+            xp, _ = activations(act, x32[plain])
+            op = torch.empty((len(plain), n), dtype=torch.float32, device="cuda")
+            jq.matmul(gpu, xp, len(plain), w, op, scratch)
+            assert np.array_equal(op.cpu().numpy(), got[plain]), ("row invariance", m, env)
+        for kk in env:
+            monkeypatch.delenv(kk)
+    # tiled plans
+    m = 40
+    x, xv = activations(act, _wide_range_rows(95, m, k, act))
+    want = O.matmul_f64(xv, dense)
+    tiled = {}
+    for plan in (jq.Plan(32, 64, 1), jq.Plan(64, 64, 1), jq.Plan(128, 128, 1), jq.Plan(256, 128, 1),
+                 jq.Plan(32, 128, 1), jq.Plan(64, 64, 4)):
+        out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matmul_plan(gpu, x, m, w, out, scratch, plan)
+        tiled[repr(plan)] = out.cpu().numpy()
+        check(tiled[repr(plan)], want, plan)
+    whole_k = [v for key, v in tiled.items() if "splits: 1" in key]
+    for v in whole_k[1:]:  # whole-K plans scale each row alike: the same bits
+        assert np.array_equal(v, whole_k[0])
+    # grouped products: 4 experts, 30 tokens x top-2
+    experts, tokens, top_k = 4, 30, 2
+    rawg = synth.weights(type_id, 96, experts * n, k)
+    wg = jq.QMatrix.upload(gpu, type_id, n, k, experts, rawg)
+    denseg = O.dequantize(type_id, rawg).reshape(experts * n, k)
+    x, xv = activations(act, _wide_range_rows(97, tokens, k, act))
+    ids = np.random.default_rng(98).integers(0, experts, tokens * top_k).astype(np.uint32)
+    want = O.grouped_product_f64(xv, denseg, ids, top_k, n)
+    for bm, bn in ((64, 64), (16, 64)):
+        g = jq.group_routes(gpu, _i32(ids), experts, bm, in_div=top_k)
+        out = torch.full((ids.size, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matmul_grouped(gpu, x, wg, g, out, bm, bn, 1, None)
+        check(out.cpu().numpy(), want, ("grouped", bm, bn))
+    for mr in (1, 2, 4):
+        g = jq.group_routes(gpu, _i32(ids), experts, mr, in_div=top_k)
+        out = torch.full((ids.size, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matvec_grouped(gpu, x, wg, g, out, mr)
+        check(out.cpu().numpy(), want, ("grouped small-row", mr))
+
