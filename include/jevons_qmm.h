@@ -49,8 +49,13 @@ enum {
 };
 
 /* Activation element type. The reference takes FP16 rows (gemm.rs:405, :537); BF16 and F32
- * rows are converted to FP16 while they are staged on chip (exact for BF16 magnitudes in
- * [2^-14, 65504]; F32 rounds to nearest even, as the reference's upload_f16 does). */
+ * rows are converted to FP16 on chip (exact for BF16 magnitudes in [2^-14, 65504]; F32 rounds to
+ * nearest even, as the reference's upload_f16 does). A row holding values beyond the FP16 range
+ * is first divided by a power of two and its outputs multiplied back, which is exact (the
+ * reference's f16_linear_scaled rule, crates/jevons-burn/src/kernels.rs:105, :120-130, with a
+ * power of two): tiled products scale rows whose largest magnitude exceeds 16384, small-row
+ * products the columns of a row in which some value overflowed FP16. Values far below the row's
+ * largest then lose low bits, as FP16 subnormals. */
 typedef enum { JV_ACT_F16 = 0, JV_ACT_BF16 = 1, JV_ACT_F32 = 2 } jv_act;
 
 /* Output element type. The reference writes FP32; BF16 rounds the FP32 sum to nearest even. */
