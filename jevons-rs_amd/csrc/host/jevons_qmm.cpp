@@ -629,7 +629,9 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         w->n * w->experts * w->k < (1ull << 32)) {
         const bool q8 = w->fmt == JV_FMT_Q8_0, q6 = w->fmt == JV_FMT_Q6K;
         const char *fname = q8 ? "q8_0" : (q6 ? "q6k" : "q4k");
-        const int mv = m == 1 ? 1 : (m == 2 ? 2 : 4);
+        // rows are spread over the four lane groups: ceil(m / 4) per group, the kernels' MV
+        const int rpg = (int)((m + 3) / 4);
+        const int mv = rpg == 1 ? 1 : (rpg == 2 ? 2 : 4);
         const int cus = std::max(1, ctx->info.compute_units);
         const int waves = q8 ? 16 : 8;
         const int ku = q8 ? 64 : 256;  // K per item
@@ -637,7 +639,7 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         const int U = (int)(w->k / ku);
         const int T = (int)(w->n / 16);
         const int umax = (U + waves - 1) / waves;
-        const int tw = q6 || m <= 2 ? 1 : 2;  // tiles per workgroup of the per-tile kernels
+        const int tw = q6 || mv < 4 ? 1 : 2;  // tiles per workgroup of the per-tile kernels
         // per wave: FP16 activations [m][ku umax + 8], sums [m][ku umax / xg], for Q6_K a zero
         // row [ku umax + 8], and m range factors. The per-tile kernels reuse it for the wave's
         // tile partials (tw KB); the persistent ones add two chunks of 2 tiles x waves partials;

@@ -889,10 +889,27 @@ __device__ __forceinline__ bool stage_wave_checked(const QmmParams &p, int c0, i
     return true;
 }
 
-// Multiplies a lane's accumulator (output rows 4g .. 4g + 3) by the rows' range factors.
+// Rows of the small-row products are spread over the four lane groups: with RPG = ceil(M / 4)
+// rows per group, row m is MFMA row 4 (m / RPG) + m % RPG, so lane group g holds rows
+// g RPG .. g RPG + RPG - 1 in accumulator elements 0 .. RPG - 1, and the per-row arithmetic
+// after each MFMA covers RPG elements instead of 4 (M = 2 to 4 cost what M = 1 costs). Each
+// output element is the same MFMA and FMA chain wherever its row sits, so the bits do not depend
+// on M. The activation row that MFMA row r reads (rows with r % 4 >= RPG feed accumulator
+// elements that are never stored, and read a real row):
+__device__ __forceinline__ int spread_row(int r, int rpg, int M) {
+    return min((r >> 2) * rpg + min(r & 3, rpg - 1), M - 1);
+}
+// Output row of accumulator element i of lane group g, or -1 for an element holding no row.
+__device__ __forceinline__ int spread_out(int g, int i, int rpg, int M) {
+    const int m = g * rpg + i;
+    return i < rpg && m < M ? m : -1;
+}
+
+// Multiplies a lane's accumulator (lane group g's rows) by the rows' range factors.
 __device__ __forceinline__ void unscale_rows(f32x4 &a, const float *Sc, int g, int M) {
+    const int rpg = (M + 3) >> 2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] *= Sc[min(4 * g + i, M - 1)];
+    for (int i = 0; i < 4; ++i) a[i] *= Sc[min(g * rpg + min(i, rpg - 1), M - 1)];
 }
 
 // One block against activations staged in LDS, with the scale arithmetic regrouped to cut
@@ -964,6 +981,68 @@ __device__ __forceinline__ void q4k_block_fast(const Q4KItem &cur, const _Float1
     for (int i = 0; i < MV; ++i) acc[i] = __builtin_fmaf(d, __builtin_fmaf(vo[i], 0.0625f, ve[i]), acc[i]);
     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[ul * 8 + g], cA, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[ul * 8 + 4 + g], cB, acc, 0, 0, 0);
+}
+
+// q4k_block_fast with the unit's activation fragments A[j] and sums xa = X_g, xb = X_{4+g} in
+// registers: the same instructions on the same values, so the same bits.
+template <int MV>
+__device__ __forceinline__ void q4k_block_regs(const Q4KItem &cur, const f16x8 A[8], float xa, float xb,
+                                               uint32_t sh, float kfac, f32x4 &acc) {
+    const uint4 hd = q4k_head_gather(cur.hv);
+    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+    // scale bytes: y = q[0..3], z = q[4..7], w = q[8..11] (quant.rs:14-23)
+    uint32_t s_lo = hd.y & 0x3f3f3f3fu;                                         // s_0..s_3
+    asm("" : "+v"(s_lo));  // opaque: each byte converts with one v_cvt_f32_ubyteN
+    const uint32_t s_hi = ((hd.y >> 2) & 0x30303030u) | (hd.w & 0x0f0f0f0fu);    // s_4..s_7
+    const uint32_t m_hi = ((hd.z >> 2) & 0x30303030u) | ((hd.w >> 4) & 0x0f0f0f0fu);  // m_4..m_7
+    const float sg = (float)((s_lo >> sh) & 0xffu), s4g = (float)((s_hi >> sh) & 0xffu);
+    const float mg = (float)((hd.z >> sh) & 63u), m4g = (float)((m_hi >> sh) & 0xffu);
+    const float kd = kfac * d;
+    const float cA = __builtin_fmaf(kd, sg, -(dmin * mg));
+    const float cB = __builtin_fmaf(kd, s4g, -(dmin * m4g));
+    float sj[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        sj[k] = (float)((s_lo >> (8 * k)) & 0xffu);
+        sj[4 + k] = (float)((s_hi >> (8 * k)) & 0xffu);
+    }
+    uint32_t magic = 0x64006400u;
+    asm("" : "+v"(magic));
+    const uint32_t w[8] = {cur.q0.x, cur.q0.y, cur.q0.z, cur.q0.w, cur.q1.x, cur.q1.y, cur.q1.z, cur.q1.w};
+    float ve[MV], vo[MV];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+        f32x4 S[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int j = 4 * hf + q;
+            const uint32_t wa = w[j & ~1], wb = w[(j & ~1) + 1];
+            const uint32_t mask = (j & 1) ? 0x00f000f0u : 0x000f000fu;
+            uint4 bq;
+            bq.x = (wa & mask) | magic;
+            bq.y = ((wa >> 8) & mask) | magic;
+            bq.z = (wb & mask) | magic;
+            bq.w = ((wb >> 8) & mask) | magic;
+            S[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[j], __builtin_bit_cast(f16x8, bq),
+                                                          f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < MV; ++i) {
+            if (hf == 0) {
+                ve[i] = sj[0] * S[0][i];
+                vo[i] = sj[1] * S[1][i];
+            } else {
+                ve[i] = __builtin_fmaf(sj[4], S[0][i], ve[i]);
+                vo[i] = __builtin_fmaf(sj[5], S[1][i], vo[i]);
+            }
+            ve[i] = __builtin_fmaf(sj[4 * hf + 2], S[2][i], ve[i]);
+            vo[i] = __builtin_fmaf(sj[4 * hf + 3], S[3][i], vo[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MV; ++i) acc[i] = __builtin_fmaf(d, __builtin_fmaf(vo[i], 0.0625f, ve[i]), acc[i]);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xa, cA, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xb, cB, acc, 0, 0, 0);
 }
 
 // Q4_K as a small-row format: item = one 256-element block of a 16-row tile.
@@ -1186,7 +1265,7 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p, int wt_off = 0) {
         // the fragment reads above the staging writes.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
-        const int arow = min(r16, p.M - 1);  // rows >= M feed output rows that are never stored
+        const int arow = spread_row(r16, (p.M + 3) >> 2, p.M);
         const _Float16 *xrow = xs + arow * stride;
         const float *Xrow = Xs + arow * xstride;
         const typename G::Lane lc = G::lane_consts(g);
@@ -1229,8 +1308,8 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p, int wt_off = 0) {
         const int col = (tile0 + t) * 16 + r16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int m = 4 * g + i;
-            if (m < p.M) {
+            const int m = spread_out(g, i, (p.M + 3) >> 2, p.M);
+            if (m >= 0) {
                 const int mo = GRP ? (int)p.ids[m] : m;  // grouped: output row ids[s]
                 const size_t o = (size_t)mo * (size_t)p.ldo + (size_t)col;
                 if (p.out_type == 0)
@@ -1279,8 +1358,8 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
         const int col = tile * 16 + r16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int m = 4 * g + i;
-            if (m < p.M) {
+            const int m = spread_out(g, i, (p.M + 3) >> 2, p.M);
+            if (m >= 0) {
                 const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
                 if (p.out_type == 0)
                     ((float *)p.out)[o] = v[i];
@@ -1338,7 +1417,7 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
             scaled = stage_wave_checked<2, XB, G::XG, false>(p, c0, nc, xs, stride, Xs, xstride, Sc, lane, issue);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 
-        const int arow = min(r16, p.M - 1);  // rows >= M feed output rows that are never stored
+        const int arow = spread_row(r16, (p.M + 3) >> 2, p.M);
         const _Float16 *xrow = xs + arow * stride;
         const float *Xrow = Xs + arow * xstride;
         const typename G::Lane lc = G::lane_consts(g);
@@ -1438,7 +1517,7 @@ __device__ __forceinline__ void qmvs_body(const QmmParams &p) {
             lds_barrier();
         }
         if (live) {
-            const int arow = min(r16, p.M - 1);  // rows >= M feed output rows that are never stored
+            const int arow = spread_row(r16, (p.M + 3) >> 2, p.M);
             const _Float16 *xrow = xs + arow * stride;
             const float *Xrow = Xs + arow * xstride;
             const typename G::Lane lc = G::lane_consts(g);
@@ -1462,10 +1541,11 @@ __device__ __forceinline__ void qmvs_body(const QmmParams &p) {
     // Partials are written and read at device scope (sc1: through to the level every compute
     // unit sees, no cache-wide write-back or invalidate); the store acknowledgements are awaited
     // before the count, and the reads are issued only after the count completes.
+    const int rpg = (p.M + 3) >> 2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int m = 4 * lg + i;
-        if (m < p.M)
+        const int m = spread_out(lg, i, rpg, p.M);
+        if (m >= 0)
             __hip_atomic_store(p.part + (size_t)s * plane + (size_t)m * p.N + col, acc[i],
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1477,8 +1557,8 @@ __device__ __forceinline__ void qmvs_body(const QmmParams &p) {
     if (((old + 16u / W) & 15u) != 0) return;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int m = 4 * lg + i;
-        if (m < p.M) {
+        const int m = spread_out(lg, i, rpg, p.M);
+        if (m >= 0) {
             float sum = 0.f;
             for (int t = 0; t < W; ++t) {
                 const float v = t == s ? acc[i]
@@ -1498,9 +1578,9 @@ __device__ __forceinline__ void qmvs_body(const QmmParams &p) {
 }  // namespace
 
 // One-tile workgroups run four per compute unit (8 waves per SIMD, at most 64 VGPRs); the
-// library takes them for M <= 2, and two-tile workgroups (half the activation staging per weight
+// library takes them for M <= 8, and two-tile workgroups (half the activation staging per weight
 // byte) for larger M where the persistent kernel does not fit. MV = output rows kept per lane
-// group (M = 1, 2, or up to 16).
+// group (rows spread over the groups: M <= 4, M <= 8, M <= 16).
 #define JV_QMV(TW, MV, XB)                                                                   \
     extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(TW == 1 ? 8 : 4))) \
     void jv_qmv_q4k_t##TW##_m##MV(QmmParams p) {                                             \
@@ -1524,14 +1604,15 @@ JV_QMV6(1, 4, 8)
     extern "C" __global__ __launch_bounds__(64 * W) void jv_qmvp_##NAME##_m##MV(QmmParams p) { \
         qmvp_body<G, W, 2, 4, MV, XB>(p);                                                    \
     }
-JV_QMVP(q4k, GQ4K, 8, 1, 2)
-JV_QMVP(q4k, GQ4K, 8, 2, 4)
+// Activation loads in flight per lane (XB) cover the rows a variant stages: up to 4, 8 or 16.
+JV_QMVP(q4k, GQ4K, 8, 1, 4)
+JV_QMVP(q4k, GQ4K, 8, 2, 8)
 JV_QMVP(q4k, GQ4K, 8, 4, 8)
-JV_QMVP(q6k, GQ6K, 8, 1, 2)
-JV_QMVP(q6k, GQ6K, 8, 2, 4)
+JV_QMVP(q6k, GQ6K, 8, 1, 4)
+JV_QMVP(q6k, GQ6K, 8, 2, 8)
 JV_QMVP(q6k, GQ6K, 8, 4, 8)
-JV_QMVP(q8_0, GQ8_0, 16, 1, 2)
-JV_QMVP(q8_0, GQ8_0, 16, 2, 4)
+JV_QMVP(q8_0, GQ8_0, 16, 1, 4)
+JV_QMVP(q8_0, GQ8_0, 16, 2, 8)
 JV_QMVP(q8_0, GQ8_0, 16, 4, 8)
 
 // Q8_0: 16 waves, each four 64-k items of a tile at K = 4096 (all in flight).
