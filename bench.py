@@ -305,47 +305,47 @@ def measure_configs(gpu, steps):
                                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
     del ms
     log("q8_0 gemv:", res["q8_0_gemv"])
-    # layer GEMMs at M = 256
+    # layer GEMMs at M = 256: a denoising block's canvas products, whose plans come from the
+    # plan tuner without the row-invariance requirement (Tuner::dense(w, m, false),
+    # tune.rs:162-174; split-K allowed); the prefill-style whole-K auto plans are timed beside
+    # them. The q, k and v projections also run as one product [8192, 3840] on their shared input.
     layers = [("q", jq.Q4K, 4096, 3840), ("k", jq.Q4K, 2048, 3840), ("v", jq.Q4K, 2048, 3840),
-              ("o", jq.Q4K, 3840, 4096), ("gate_up", jq.Q4K, 30720, 3840), ("down", jq.Q6K, 3840, 15360)]
+              ("o", jq.Q4K, 3840, 4096), ("gate_up", jq.Q4K, 30720, 3840), ("down", jq.Q6K, 3840, 15360),
+              ("qkv", jq.Q4K, 4096 + 2 * 2048, 3840)]
     m = 256
-    per, tsum, fsum = {}, 0.0, 0.0
+    tuner = jq.Tuner.new(gpu, None)
+    per = {}
     for name, kind, n, k in layers:
         ms, _ = mats(kind, n, k, 2, 5)
         x = xrows(m, k, 2)
         out = torch.empty((m, n), dtype=torch.float32, device="cuda")
-        plan = jq.Plan.auto(ms[0], m, row_invariant=True)
-        jq.matmul_plan(gpu, x, m, ms[0], out, scratch, plan)
-        t = kernel_time_ms(lambda r: jq.matmul_plan(gpu, x, m, ms[r % 2], out, scratch, plan),
-                           max(4, steps // 4))
-        flops = 2.0 * m * n * k
-        per[name] = {"n": n, "k": k, "format": "Q6_K" if kind == jq.Q6K else "Q4_K",
-                     "plan": [plan.bm, plan.bn, plan.splits], "us": round(t * 1e3, 2),
-                     "tflops": round(flops / (t * 1e-3) / 1e12, 1)}
-        tsum += t
-        fsum += flops
+        tuner.tune_dense(ms, m, False, x, out, scratch)
+        row = {"n": n, "k": k, "format": "Q6_K" if kind == jq.Q6K else "Q4_K", "gflop": round(2e-9 * m * n * k, 3)}
+        for mode, plan in (("canvas", tuner.dense(ms[0], m, False)), ("prefill", jq.Plan.auto(ms[0], m, row_invariant=True))):
+            jq.matmul_plan(gpu, x, m, ms[0], out, scratch, plan)
+            t = kernel_time_ms(lambda r: jq.matmul_plan(gpu, x, m, ms[r % 2], out, scratch, plan), max(4, steps // 4))
+            row[mode] = {"plan": [plan.bm, plan.bn, plan.splits], "us": round(t * 1e3, 2),
+                         "tflops": round(2.0 * m * n * k / (t * 1e-3) / 1e12, 1)}
+        per[name] = row
         del ms
-    tf = fsum / (tsum * 1e-3) / 1e12
-    # the q, k and v projections as one Q4_K product [8192, 3840] on their shared input
-    n, k = 4096 + 2 * 2048, 3840
-    ms, _ = mats(jq.Q4K, n, k, 2, 5)
-    x = xrows(m, k, 2)
-    out = torch.empty((m, n), dtype=torch.float32, device="cuda")
-    plan = jq.Plan.auto(ms[0], m, row_invariant=True)
-    jq.matmul_plan(gpu, x, m, ms[0], out, scratch, plan)
-    t = kernel_time_ms(lambda r: jq.matmul_plan(gpu, x, m, ms[r % 2], out, scratch, plan), max(4, steps // 4))
-    fflops = 2.0 * m * n * k
-    fused = {"n": n, "k": k, "format": "Q4_K", "plan": [plan.bm, plan.bn, plan.splits], "us": round(t * 1e3, 2),
-             "tflops": round(fflops / (t * 1e-3) / 1e12, 1),
-             "separate_qkv_us": round(sum(per[nm]["us"] for nm in ("q", "k", "v")), 2)}
-    del ms
-    res["layer_gemms_m256"] = {"workload": "one transformer block's six GEMMs at M=256, bf16 activations, f32 out",
-                               "gemms": per, "fused_qkv": fused, "total_us": round(tsum * 1e3, 2),
-                               "total_us_fused_qkv": round((tsum - sum(per[nm]["us"] for nm in ("q", "k", "v")) * 1e-3
-                                                            + t) * 1e3, 2),
-                               "roofline": {"bound": "mfma", "achieved": round(tf, 1),
-                                            "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                            "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}}
+    six = ("q", "k", "v", "o", "gate_up", "down")
+    fused = ("qkv", "o", "gate_up", "down")
+    flops = sum(2.0 * m * per[nm]["n"] * per[nm]["k"] for nm in six)
+
+    def total(names, mode):
+        return sum(per[nm][mode]["us"] for nm in names)
+
+    tf = flops / (total(fused, "canvas") * 1e-6) / 1e12
+    res["layer_gemms_m256"] = {
+        "workload": "one transformer block's six GEMMs at M=256 (a denoising block), bf16 activations, "
+                    "f32 out; canvas plans from the tuner (split-K allowed), q/k/v fused into one product",
+        "gemms": per,
+        "total_us": round(total(fused, "canvas"), 2),
+        "total_us_separate_qkv": round(total(six, "canvas"), 2),
+        "total_us_prefill_plans": round(total(six, "prefill"), 2),
+        "total_us_prefill_plans_fused_qkv": round(total(fused, "prefill"), 2),
+        "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}}
     log("layer gemms:", res["layer_gemms_m256"])
     # Q6_K vocabulary projection and argmax
     n, k = 262144, 3840

@@ -540,24 +540,36 @@ bool reg_format(const jv_qmatrix *w) {
     return w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0;
 }
 
+// Split-K slices of the generic kernel (format units [z U / splits, (z + 1) U / splits)) that
+// are whole 256-element blocks, so the pipelined tiles can run them with the same bits.
+bool block_slices(const jv_qmatrix *w, uint32_t splits) {
+    const size_t ku = (size_t)fmt_unit(w->fmt), units = w->k / ku;
+    if (w->k % 256 != 0 || splits < 1 || w->k / 256 < splits) return false;
+    for (size_t z = 1; z < splits; ++z)
+        if (z * units / splits * ku % 256 != 0) return false;
+    return true;
+}
+
 bool pipelined_plan(const jv_qmatrix *w, jv_plan plan) {
-    return plan.splits == 1 && w->k % 256 == 0 &&
+    return w->k % 256 == 0 && block_slices(w, plan.splits) &&
            ((plan.bm == 256 && plan.bn == 128) || (plan.bm == 128 && plan.bn == 128) ||
             (plan.bm == 64 && plan.bn == 64) || (reg_format(w) && plan.bm == 32 && plan.bn == 64));
 }
 
-// `fixed` (the array of jv_matmul_noalloc, or null) holds the packed activations in place of the
-// context's own buffer.
+// `scratch` holds the split-K partials (plans with splits > 1); when it is the fixed array of
+// jv_matmul_noalloc, it also holds the packed activations in place of the context's buffer.
 jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, const jv_qmatrix *w,
                            void *out, jv_out out_type, jv_plan plan, void *stream,
-                           const GroupArgs *grp, jv_scratch *fixed = nullptr) {
+                           const GroupArgs *grp, jv_scratch *scratch = nullptr) {
     jv_status st = JV_OK;
+    if (grp && plan.splits > 1) return fail(JV_ERR_INVALID, "grouped pipelined tiles do not split K");
     const int jobs_or_tiles = grp ? (int)grp->max_jobs : (int)((m + plan.bm - 1) / plan.bm);
     const int mtiles = jobs_or_tiles * (int)(plan.bm / 16);
     // fragments, then each packed row's range factor
     const size_t frag_bytes = (size_t)mtiles * 16 * w->k * 2;
-    void *pack = nullptr, *none = nullptr;
-    st = stage_buffers(ctx, fixed, frag_bytes + (size_t)mtiles * 16 * 4, 0, &pack, &none);
+    const size_t part_bytes = plan.splits > 1 ? (size_t)plan.splits * m * w->n * 4 : 0;
+    void *pack = nullptr, *partials = nullptr;
+    st = stage_buffers(ctx, scratch, frag_bytes + (size_t)mtiles * 16 * 4, part_bytes, &pack, &partials);
     if (st != JV_OK) return st;
     float *rscale = (float *)((uint8_t *)pack + frag_bytes);
     st = launch_pack(ctx, x, act, m, w->k, mtiles, 0, (uint16_t *)pack, rscale, grp, plan.bm, stream);
@@ -574,6 +586,9 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     gp.K = (int32_t)w->k;
     gp.ldo = (int32_t)(w->n);
     gp.out_type = (int32_t)out_type;
+    gp.splits = (int32_t)plan.splits;
+    gp.part = (float *)partials;
+    gp.split_stride = (int64_t)(m * w->n);
     if (grp) {
         gp.ids = grp->ids;
         gp.offsets = grp->offsets;
@@ -595,8 +610,15 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
              w8 ? "r8" : (reg ? "r" : ""));
     const unsigned waves = plan.bm >= 128 || w8 ? 8 : 4;
     const size_t glds = 4 * ((reg ? 0 : plan.bm) + plan.bn) / 16 * 1024;
-    return launch(ctx, name, dim3((unsigned)(w->n / plan.bn), (unsigned)jobs_or_tiles),
-                  dim3(64 * waves), glds, stream, gargs);
+    st = launch(ctx, name, dim3((unsigned)(w->n / plan.bn), (unsigned)jobs_or_tiles, plan.splits),
+                dim3(64 * waves), glds, stream, gargs);
+    if (st != JV_OK || plan.splits == 1) return st;
+    const void *part = partials;
+    int64_t len = (int64_t)(m * w->n);
+    int sp = (int)plan.splits, ot = (int)out_type;
+    void *rargs[] = {&part, &out, &len, &sp, &ot};
+    return launch(ctx, "jv_reduce_splits", dim3((unsigned)((len + 255) / 256)), dim3(256), 0,
+                  stream, rargs);
 }
 
 jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
@@ -724,8 +746,7 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         }
     }
     if (pipelined_plan(w, plan))
-        return launch_pipelined(ctx, x, act, m, w, out, out_type, plan, stream, nullptr,
-                                scratch && scratch->fixed ? scratch : nullptr);
+        return launch_pipelined(ctx, x, act, m, w, out, out_type, plan, stream, nullptr, scratch);
     return launch_tiles(ctx, x, act, m, w, out, out_type, scratch, plan, stream, nullptr);
 }
 
@@ -983,6 +1004,25 @@ jv_plan jv_plan_heuristic(const jv_qmatrix *w, size_t m, int row_invariant, size
 // gfx950 choice: the small-row kernel up to 16 rows; otherwise the row tile that covers m with
 // the least padding, then the widest column tile that still gives every compute unit a
 // workgroup, then (outside prefill) split-K until the grid fills the device.
+// Products outside prefill may split K (their rows may then differ by plan, as the reference
+// allows for canvas products, tune.rs:170-173). Long K (8192 and more) takes the 256- or
+// 128-row tile and enough slices to give every compute unit a workgroup: each weight is then
+// decoded once per 256 rows and the activations are read by half as many column tiles (down
+// projection, K = 15360 at m = 256: 67 us on 256 x 128 / 8 against 100 us on whole-K 64 x 64).
+// Otherwise a tile whose workgroups fill less than three quarters of the device doubles its
+// slices until they fill it (k and v projections, 2048 x 3840 at m = 256: 64 x 64 / 2, 26
+// against 29 us). Slices stay whole 256-element blocks, at least four of them.
+static jv_plan canvas_split(const jv_qmatrix *w, size_t m, jv_plan p, size_t cus) {
+    if (w->k >= 8192 && m >= 128 && w->n % 128 == 0) p = m >= 192 ? jv_plan{256, 128, 1} : jv_plan{128, 128, 1};
+    const size_t wgs = (w->n / p.bn) * ((m + p.bm - 1) / p.bm);
+    if (w->k >= 8192 || wgs * 4 < cus * 3) {
+        uint32_t s = 1;
+        while (wgs * s < cus && w->k / 256 / (2 * s) >= 4 && block_slices(w, 2 * s)) s *= 2;
+        p.splits = s;
+    }
+    return p;
+}
+
 jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
     if (!w) return jv_plan{0, 0, 0};
     // The small-row kernel keeps a row's bits independent of m but not equal to the tile
@@ -997,17 +1037,21 @@ jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
     // of a narrow matrix outside prefill keep the generic tiles, whose split-K fills the device.
     const size_t tiles64 = (cols / 64) * ((m + 63) / 64);
     if (w->k % 256 == 0 && (m >= 48 || row_invariant || tiles64 >= cus)) {
+        jv_plan p{0, 0, 1};
         // 256 x 128 from 192 rows (at most a quarter of its rows padding), 128 x 128 above 64
         // rows, each only while its workgroups still fill the device (gate_up at m = 128:
         // 55 us on 128 x 128 against 69 us on 256 x 128 and 60 us on 64 x 64)
         if (cols % 128 == 0 && m >= 192 && ((m + 255) / 256) * (cols / 128) * 16 >= cus * 15)
-            return jv_plan{256, 128, 1};
-        if (cols % 128 == 0 && m > 64 && ((m + 127) / 128) * (cols / 128) * 16 >= cus * 15)
-            return jv_plan{128, 128, 1};
+            p = jv_plan{256, 128, 1};
+        else if (cols % 128 == 0 && m > 64 && ((m + 127) / 128) * (cols / 128) * 16 >= cus * 15)
+            p = jv_plan{128, 128, 1};
         // up to 32 rows: half a 64-row tile would be padding (Q6_K vocabulary projection at
         // m = 32: 235 us against 281 us on 64 x 64; Q8_0 4096 x 4096: 25 against 29 us)
-        if (cols % 64 == 0 && m <= 32 && reg_format(w)) return jv_plan{32, 64, 1};
-        if (cols % 64 == 0) return jv_plan{64, 64, 1};
+        else if (cols % 64 == 0 && m <= 32 && reg_format(w))
+            p = jv_plan{32, 64, 1};
+        else if (cols % 64 == 0)
+            p = jv_plan{64, 64, 1};
+        if (p.bm != 0) return row_invariant ? p : canvas_split(w, m, p, cus);
     }
     const uint32_t bm = m <= 32 ? 32 : (m <= 64 ? 64 : 128);
     const size_t mtiles = (m + bm - 1) / bm;
@@ -1031,8 +1075,8 @@ jv_plan jv_plan_auto(const jv_qmatrix *w, size_t m, int row_invariant) {
 int jv_plan_valid(const jv_qmatrix *w, size_t m, jv_plan p) {
     if (!w) return 0;
     if (p.bm == 0) return m <= 16 && p.splits == 1;
-    // gfx950 tile: 256 rows x 128 columns, whole K (no split)
-    if (p.bm == 256) return p.bn == 128 && p.splits == 1 && w->n % 128 == 0 && w->k % 256 == 0;
+    // gfx950 tile: 256 rows x 128 columns, split-K only in whole 256-element blocks
+    if (p.bm == 256) return p.bn == 128 && w->n % 128 == 0 && block_slices(w, p.splits) && p.splits <= 16;
     const bool bm_ok = p.bm == 32 || p.bm == 64 || p.bm == 128;
     const bool bn_ok = p.bn == 64 || p.bn == 128 || p.bn == 256;
     return bm_ok && bn_ok && w->n % p.bn == 0 && p.splits >= 1 && p.splits <= 16 &&
@@ -1167,7 +1211,7 @@ jv_status jv_matmul_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len
     GroupArgs ga{g->ids, g->offsets, g->jobs, g->max_jobs, g->in_div, bm};
     // 64 x 64 and 128 x 128 jobs on the pipelined tiles (same bits as the generic tiles) while
     // the per-job packed activations stay within 1 GiB
-    if (bm != 256 && pipelined_plan(w, jv_plan{bm, bn, splits}) &&
+    if (bm != 256 && splits == 1 && pipelined_plan(w, jv_plan{bm, bn, splits}) &&
         g->max_jobs * bm * w->k * 2 <= (1ull << 30))
         return launch_pipelined(ctx, x, act, g->rows, w, out, out_type, jv_plan{bm, bn, splits},
                                 stream, &ga);

@@ -141,7 +141,8 @@ double time_runs(Run run, jv_status *st) {
 
 // Candidate plans (tune.rs:499-530, with the gfx950 tiles added): the small-row kernel for
 // m <= 16 when rows may vary in bits, every reference tile that fits the rows, split-K only
-// when row invariance is not asked for, and the pipelined whole-K tiles.
+// when row invariance is not asked for, and the pipelined tiles (256 x 128 also split in
+// whole 256-element blocks outside prefill).
 std::vector<jv_plan> dense_candidates(const jv_qmatrix *w, size_t m, int row_invariant) {
     uint32_t fmt;
     size_t n, k, experts;
@@ -159,8 +160,9 @@ std::vector<jv_plan> dense_candidates(const jv_qmatrix *w, size_t m, int row_inv
             }
         }
     }
-    for (jv_plan p : {jv_plan{256, 128, 1}, jv_plan{128, 128, 1}, jv_plan{64, 64, 1}})
-        if (jv_plan_valid(w, m, p) &&
+    for (jv_plan p : {jv_plan{256, 128, 1}, jv_plan{128, 128, 1}, jv_plan{64, 64, 1}, jv_plan{256, 128, 2},
+                      jv_plan{256, 128, 4}, jv_plan{256, 128, 8}})
+        if ((p.splits == 1 || !row_invariant) && jv_plan_valid(w, m, p) &&
             std::none_of(out.begin(), out.end(), [&](const jv_plan &q) {
                 return q.bm == p.bm && q.bn == p.bn && q.splits == p.splits;
             }))

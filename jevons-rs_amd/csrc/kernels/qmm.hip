@@ -2021,6 +2021,9 @@ struct DF {  // any format with the F* interface of the small-tile kernel
 // from LDS; the reads for stage t + 1 are issued while stage t's MFMAs run, and stage t + 2 is
 // written meanwhile. Raw weights are loaded 8 stages ahead. Register slots are ordered
 // own-first, so which fragment is whose is fixed at compile time. Requires K % 256 == 0.
+// Split-K (grid z, ungrouped): slice z runs the same pipeline over its own K units, the generic
+// kernel's slice z (whole 256-element blocks), from a zero accumulator, and writes its FP32
+// partial for jv_reduce_splits; so a split plan gives the generic kernel's bits.
 //
 // Each output element is the same MFMA chain over K as in the other tiled kernels (32-k steps
 // in order, lane group g holding k 32s + 8g .. +8), so the result is bitwise identical to theirs.
@@ -2043,7 +2046,11 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, r = lane & 15;
     const int mq = w / WN, nh = w % WN;
-    const int U8 = p.K >> 8;          // blocks of 8 stages
+    // this slice's K units (the whole K without split-K), in blocks of 8 stages
+    const int U_all = (p.K >> 5) / D::SPU;
+    const int uf = (int)((int64_t)blockIdx.z * U_all / p.splits);
+    const int zb0 = uf / UPS;                                                         // first block
+    const int U8 = ((int)((int64_t)(blockIdx.z + 1) * U_all / p.splits) - uf) / UPS;  // blocks
     const int UK = U8 * UPS;          // K units
     const int mt0 = blockIdx.y * TM;  // first 16-row activation tile
     const int t0 = blockIdx.x * TN;   // first 16-row weight tile
@@ -2058,6 +2065,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
         wt0 = (int)e * (p.N >> 4);
     }
     const int stages = 8 * U8;
+    const size_t stot = (size_t)(p.K >> 5);  // stages of the whole K
     const uint32_t lo16 = (uint32_t)lane * 16u;  // this lane's bytes in a 1 KB fragment
 
     // Local m-tile of slot i: own slots first (the AS this wave stages), then the rest of the
@@ -2076,7 +2084,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     const uint8_t *xa_own[AS];
 #pragma unroll
     for (int i = 0; i < AS; ++i)
-        xa_own[i] = (const uint8_t *)p.xa + (size_t)(mt0 + m_of(i)) * (size_t)stages * 1024u + lo16;
+        xa_own[i] = (const uint8_t *)p.xa + ((size_t)(mt0 + m_of(i)) * stot + 8 * (size_t)zb0) * 1024u + lo16;
     auto load_a = [&](u32x4 *dst, int st) __attribute__((always_inline)) {
         const uint32_t off = (uint32_t)min(st, stages - 1) * 1024u;
 #pragma unroll
@@ -2096,7 +2104,8 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 #pragma unroll
         for (int q = 0; q < UPS; ++q)
 #pragma unroll
-            for (int k = 0; k < BS; ++k) D::load(dst[q][k], p, wt0 + t0 + n_of(k), min(UPS * b + q, UK - 1), g, r);
+            for (int k = 0; k < BS; ++k)
+                D::load(dst[q][k], p, wt0 + t0 + n_of(k), UPS * zb0 + min(UPS * b + q, UK - 1), g, r);
     };
     typename D::Prep pp[UPS][BS];
     auto block_prep = [&](const typename D::Raw (*it)[BS]) __attribute__((always_inline)) {
@@ -2236,7 +2245,9 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
                 if (live) {
                     const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
                     const float v = acc[i][k][e] * p.rscale[pr];  // exact: a power of two
-                    if (f32_out)
+                    if (p.splits > 1)
+                        p.part[(int64_t)blockIdx.z * p.split_stride + (int64_t)o] = v;
+                    else if (f32_out)
                         ((float *)p.out)[o] = v;
                     else
                         ((uint16_t *)p.out)[o] = (uint16_t)f2bf(v);
@@ -2267,19 +2278,24 @@ __device__ __forceinline__ void gemm8_body(const GemmParams &p) {
     const int g = lane >> 4, r = lane & 15;
     const int mq = w >> 1, nh = w & 1;   // compute: m-tile mq, n-tiles 2 nh and 2 nh + 1
     const int par = w >> 2, dq = w & 3;  // decode: n-tile dq of the stages of parity par
-    const int U8 = p.K >> 8;
+    // this slice's K units (the whole K without split-K), in blocks of 8 stages
+    const int U_all = (p.K >> 5) / D::SPU;
+    const int uf = (int)((int64_t)blockIdx.z * U_all / p.splits);
+    const int zb0 = uf / UPS;
+    const int U8 = ((int)((int64_t)(blockIdx.z + 1) * U_all / p.splits) - uf) / UPS;
     const int UK = U8 * UPS;
     const int stages = 8 * U8;
     const int mt0 = blockIdx.y * 4, t0 = blockIdx.x * 4;
     const uint32_t lo16 = (uint32_t)lane * 16u;
-    const uint8_t *xa = (const uint8_t *)p.xa + (size_t)(mt0 + mq) * (size_t)stages * 1024u + lo16;
+    const uint8_t *xa = (const uint8_t *)p.xa +
+                        ((size_t)(mt0 + mq) * (size_t)(p.K >> 5) + 8 * (size_t)zb0) * 1024u + lo16;
     auto load_a = [&](u32x4 &dst, int st) __attribute__((always_inline)) {
         dst = *(const u32x4 *)(xa + (uint32_t)min(st, stages - 1) * 1024u);
     };
     auto buf_of = [&](int st) __attribute__((always_inline)) { return smem + (st & 3) * 4096 + lo16; };
     auto load_w = [&](typename D::Raw *dst, int b) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < UPS; ++q) D::load(dst[q], p, t0 + dq, min(UPS * b + q, UK - 1), g, r);
+        for (int q = 0; q < UPS; ++q) D::load(dst[q], p, t0 + dq, UPS * zb0 + min(UPS * b + q, UK - 1), g, r);
     };
     typename D::Prep pp[UPS];
     auto block_prep = [&](const typename D::Raw *it) __attribute__((always_inline)) {
@@ -2345,7 +2361,9 @@ __device__ __forceinline__ void gemm8_body(const GemmParams &p) {
             if (m < p.M) {
                 const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
                 const float v = acc[k][e] * p.rscale[m];  // exact: a power of two
-                if (f32_out)
+                if (p.splits > 1)
+                    p.part[(int64_t)blockIdx.z * p.split_stride + (int64_t)o] = v;
+                else if (f32_out)
                     ((float *)p.out)[o] = v;
                 else
                     ((uint16_t *)p.out)[o] = (uint16_t)f2bf(v);

@@ -75,6 +75,12 @@ struct GemmParams {
     // start at expert * N, and its output rows are ids[start + r] (QmmParams' job format).
     const uint32_t *ids, *offsets, *jobs;
     int32_t grouped, rows_cap;
+    // Split-K (ungrouped): grid z = slice; slice z covers the format's K units
+    // [z U / splits, (z + 1) U / splits), each a whole number of 256-element blocks, and writes
+    // FP32 partials to part + z * split_stride ([M][ldo]), summed by jv_reduce_splits.
+    float *part;
+    int64_t split_stride;
+    int32_t splits;
 };
 
 // GGML blocks (device copy of the upload) -> device layout.

@@ -229,6 +229,35 @@ def test_every_plan_matches_oracle_and_tiles_are_row_invariant(gpu, name, type_i
     assert np.array_equal(gemv_rows[3], gemv_rows[16][:3])
 
 
+@pytest.mark.parametrize("name,type_id", FORMATS)
+def test_split_k_pipelined_tiles_equal_the_generic_tiles(gpu, name, type_id):
+    # Split plans of the pipelined tiles (each slice whole 256-element blocks) against the same
+    # splits on the generic kernel (64 x 128): each slice is the same MFMA chain from zero and
+    # the partials are summed in the same order, so the bits agree
+    n, k = 512, 3072
+    w, raw = make_matrix(gpu, type_id, n, k, seed=11)
+    scratch = jq.SplitScratch(gpu)
+    for m in (37, 100, 256):
+        x, xv = activations("bf16", synth.normal_rows(5, m, k))
+        want = oracle_product(type_id, raw, n, k, xv)
+        for splits in (2, 3, 4):
+            reference = None
+            for plan in (jq.Plan(64, 128, splits), jq.Plan(64, 64, splits), jq.Plan(128, 128, splits),
+                         jq.Plan(256, 128, splits), jq.Plan(32, 64, splits)):
+                if not plan.valid_for(w, m):
+                    continue
+                say(name, "m", m, plan)
+                out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+                jq.matmul_plan(gpu, x, m, w, out, scratch, plan)
+                got = out.cpu().numpy()
+                e = err(got, want)
+                assert e <= TOL, f"m={m} {plan}: normalized error {e:.2e}"
+                if reference is None:
+                    reference = got
+                else:
+                    assert np.array_equal(reference, got), f"m={m} {plan} differs from the generic split"
+
+
 @pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0)])
 def test_small_row_product_of_wide_matrices(gpu, name, type_id):
     """Matrices with at least 8 tiles of 16 rows per compute unit take the persistent small-row
@@ -961,13 +990,17 @@ def test_plan_rules_follow_the_reference(gpu):
     for m in (1, 4, 16, 70):
         p = jq.Plan.auto(w, m, row_invariant=True)
         assert p.bm > 0 and p.splits == 1 and p.valid_for(w, m), (m, p)
-    # the gfx950 256 x 128 tile: any format, whole K in 256-element blocks, no split-K
+    # the gfx950 256 x 128 tile: any format, whole K in 256-element blocks, split-K only in whole
+    # blocks (the generic kernel's slices, z U / splits units)
     assert jq.Plan(256, 128, 1).valid_for(w, 512)
     w320 = jq.QMatrix.upload(gpu, jq.Q8_0, 256, 320, 1, synth.weights(jq.Q8_0, 1, 256, 320))
     assert not jq.Plan(256, 128, 1).valid_for(w320, 512)
     w4 = jq.QMatrix.upload(gpu, jq.Q4K, 256, 512, 1, synth.weights(jq.Q4K, 1, 256, 512))
-    assert jq.Plan(256, 128, 1).valid_for(w4, 512)
-    assert not jq.Plan(256, 128, 2).valid_for(w4, 512) and not jq.Plan(256, 64, 1).valid_for(w4, 512)
+    assert jq.Plan(256, 128, 1).valid_for(w4, 512) and jq.Plan(256, 128, 2).valid_for(w4, 512)
+    assert not jq.Plan(256, 128, 4).valid_for(w4, 512) and not jq.Plan(256, 64, 1).valid_for(w4, 512)
+    w8 = jq.QMatrix.upload(gpu, jq.Q8_0, 256, 3840, 1, synth.weights(jq.Q8_0, 1, 256, 3840))
+    assert jq.Plan(256, 128, 3).valid_for(w8, 512)  # slices of 20 units (1280 k)
+    assert not jq.Plan(256, 128, 8).valid_for(w8, 512)  # 60 units: a slice boundary at 448 k
 
 
 # ------------------------------------------------------------------ activations beyond FP16

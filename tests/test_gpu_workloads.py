@@ -4,7 +4,8 @@ f64 matmul):
 - one transformer block's six products at M = 256 at their real shapes (Q4_K q, k, v, o,
   gate_up; Q6_K down, K = 15360), and the fused q/k/v projection (N = 4096 + 2 * 2048) the
   reference runs as three launches on one input
-  (crates/jevons-gemma4-diffusion/src/model.rs:808-812);
+  (crates/jevons-gemma4-diffusion/src/model.rs:808-812), on the prefill (whole-K, row
+  invariant) plans and on the canvas plans that may split K;
 - the Q6_K vocabulary projection over the whole vocabulary (K = 3840, N = 262144) at M = 1, 8
   (persistent small-row kernels) and 32 (32 x 64 tiles), with the per-row argmax of the raw and
   of the soft-capped logits (greedy, crates/jevons-core/src/model.rs:207-219; softcap,
@@ -69,6 +70,38 @@ def test_layer_product_m256_at_its_shape(gpu, name, kind, n, k):
         if other == plan or not other.valid_for(w, m):
             continue
         assert torch.equal(_product(gpu, x, m, w, n, other), out), (name, other)
+
+
+CANVAS = LAYER + [("qkv", jq.Q4K, 8192, 3840)]
+
+
+@pytest.mark.parametrize("name,kind,n,k", CANVAS, ids=[l[0] for l in CANVAS])
+def test_layer_product_m256_canvas_plans(gpu, name, kind, n, k):
+    """The denoising block's canvas plans (row invariance not asked for, split-K allowed:
+    Tuner::dense(w, m, false), tune.rs:162-174) at the product's real shape: the library's
+    auto plan and the split pipelined tiles the tuner measures, 32 sampled rows each against the
+    f64 oracle; a split pipelined plan equals the generic kernel's split of the same slices."""
+    m = LAYER_M
+    raw = synth.weights(kind, 5, n, k)
+    w = jq.QMatrix.upload(gpu, kind, n, k, 1, raw)
+    x, xv = _layer_inputs(k)
+    rows = np.sort(np.random.default_rng(13).choice(m, 32, replace=False))
+    want = oracle_product(kind, raw, n, k, xv[rows])
+    scratch = jq.SplitScratch(gpu)
+    auto = jq.Plan.auto(w, m, row_invariant=False)
+    plans = [auto] + [p for p in (jq.Plan(64, 64, 2), jq.Plan(128, 128, 4), jq.Plan(256, 128, 8)) if p != auto]
+    for plan in plans:
+        if not plan.valid_for(w, m):
+            continue
+        out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matmul_plan(gpu, x, m, w, out, scratch, plan)
+        e = err(out.cpu().numpy()[rows], want)
+        say(name, n, k, "canvas plan", plan, "auto" if plan == auto else "", "normalized error", e)
+        assert e <= TOL, (name, plan)
+        if plan.splits > 1 and plan.bm == 64:
+            generic = torch.empty_like(out)
+            jq.matmul_plan(gpu, x, m, w, generic, scratch, jq.Plan(64, 128, plan.splits))
+            assert torch.equal(generic, out), (name, plan)
 
 
 def test_fused_qkv_projection_equals_the_three_products(gpu):
