@@ -134,7 +134,8 @@ int jv_plan_valid(const jv_qmatrix *w, size_t m, jv_plan plan);
 jv_status jv_scratch_new(jv_ctx *ctx, jv_scratch **out);
 void jv_scratch_free(jv_scratch *s);
 
-/* out[m, n] = x[m, k] . W^T with this library's plan (matmul, gemm.rs:1069-1088). */
+/* out[m, n] = x[m, k] . W^T with this library's plan (matmul, gemm.rs:1069-1088). A plan that
+ * splits K stages its partials in `scratch`, or in a buffer the context owns when it is null. */
 jv_status jv_matmul(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
                     const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
                     jv_scratch *scratch, void *stream);
@@ -147,7 +148,9 @@ jv_status jv_matmul(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t
  * kernels are jv_matmul's with a scratch buffer, but every staging buffer (packed activations of
  * the tiled products, split-K partials and tile counters) lives in one fixed device array of
  * JV_NOALLOC_SCRATCH_BYTES per GPU, set up by jv_open. The call allocates and frees no memory.
- * A product that needs more staging than the array holds is rejected with JV_ERR_INVALID (the
+ * A split-K tile plan whose staging would not fit runs with whole K on the same tile instead
+ * (then its bits can differ from jv_matmul's, within the products' accuracy). A product that
+ * still needs more staging than the array holds is rejected with JV_ERR_INVALID (the
  * message names the bytes needed and the limit). All calls on one GPU share that GPU's array,
  * which keeps the last call's contents: calls that overlap on one GPU (on other streams, or from
  * other contexts or threads) race. */

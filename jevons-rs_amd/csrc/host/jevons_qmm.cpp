@@ -540,6 +540,15 @@ bool reg_format(const jv_qmatrix *w) {
     return w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0;
 }
 
+// The context's own scratch buffer, for products given none that need one.
+jv_scratch *own_scratch(jv_ctx *ctx) {
+    if (!ctx->own) {
+        ctx->own = new jv_scratch();
+        ctx->own->ctx = ctx;
+    }
+    return ctx->own;
+}
+
 // Split-K slices of the generic kernel (format units [z U / splits, (z + 1) U / splits)) that
 // are whole 256-element blocks, so the pipelined tiles can run them with the same bits.
 bool block_slices(const jv_qmatrix *w, uint32_t splits) {
@@ -686,13 +695,8 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         const bool fsplit = force && force[0] == '1', fnosplit = force && force[0] == '0';
         // A product given no scratch buffer (jv_matvec) whose only fitting small-row kernel is
         // split-K uses the context's own, so that its rows keep the bits of every other m.
-        if (!scratch && lds_tile > lmax && !(wide && lds_persist <= lmax) && stage + 64 <= lmax) {
-            if (!ctx->own) {
-                ctx->own = new jv_scratch();
-                ctx->own->ctx = ctx;
-            }
-            scratch = ctx->own;
-        }
+        if (!scratch && lds_tile > lmax && !(wide && lds_persist <= lmax) && stage + 64 <= lmax)
+            scratch = own_scratch(ctx);
         const bool split_ok = scratch && U >= waves && (size_t)T <= kCounterTiles && stage + 64 <= lmax;
         // Persistent workgroups stage the activations once for several tiles: they serve wide
         // matrices and, above 2 rows, any matrix (at m = 4-8 on the decode shapes 10-34% faster
@@ -1105,8 +1109,11 @@ jv_status jv_matmul(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t
                     const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
                     jv_scratch *scratch, void *stream) {
     if (!w) return fail(JV_ERR_INVALID, "null weight matrix");
-    return run_product(ctx, x, act, x_len, m, w, out, out_type, out_len,
-                       jv_plan_auto(w, m, 0), scratch, stream);
+    if (!ctx) return fail(JV_ERR_INVALID, "null context");
+    // a split-K plan given no scratch buffer stages its partials in the context's own
+    const jv_plan plan = jv_plan_auto(w, m, 0);
+    if (plan.splits > 1 && !scratch) scratch = own_scratch(ctx);
+    return run_product(ctx, x, act, x_len, m, w, out, out_type, out_len, plan, scratch, stream);
 }
 
 jv_status jv_matmul_noalloc(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
@@ -1126,8 +1133,15 @@ jv_status jv_matmul_noalloc(jv_ctx *ctx, const void *x, jv_act act, size_t x_len
     fixed.buf = ptr;
     fixed.bytes = JV_NOALLOC_SCRATCH_BYTES;
     fixed.fixed = true;
-    return run_product(ctx, x, act, x_len, m, w, out, out_type, out_len, jv_plan_auto(w, m, 0), &fixed,
-                       stream);
+    // A split-K tile plan whose activations and partials would not fit in the array runs with
+    // whole K instead (same tile, no partials).
+    jv_plan plan = jv_plan_auto(w, m, 0);
+    if (plan.bm != 0 && plan.splits > 1) {
+        const size_t rows = (m + plan.bm - 1) / plan.bm * plan.bm;
+        const size_t need = align_up(rows * w->k * 2 + rows * 4, 256) + (size_t)plan.splits * m * w->n * 4;
+        if (need > JV_NOALLOC_SCRATCH_BYTES - kCounterBytes) plan.splits = 1;
+    }
+    return run_product(ctx, x, act, x_len, m, w, out, out_type, out_len, plan, &fixed, stream);
 }
 
 jv_status jv_matmul_plan(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,

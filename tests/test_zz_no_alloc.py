@@ -70,3 +70,29 @@ def test_noalloc_rejects_staging_beyond_the_array(gpu):
     torch.cuda.synchronize()
     assert not out.any()
     _compare(gpu, w, jq.Q4K, n, k, 64, 7)
+
+
+def test_noalloc_split_plan_beyond_the_array_runs_whole_k(gpu):
+    # the down projection's canvas plan at M = 256 splits K = 15360 eight ways (31.5 MB of
+    # partials beside 7.9 MB of packed activations): beyond the array, so the product runs the
+    # same 256 x 128 tile with whole K, whose staging fits
+    n, k, m = 3840, 15360, 256
+    w = _upload(gpu, jq.Q6K, n, k, 4)
+    plan = jq.Plan.auto(w, m, row_invariant=False)
+    say("noalloc fallback", plan)
+    assert plan.splits > 1 and plan.splits * m * n * 4 + m * k * 2 > jq.NOALLOC_SCRATCH_BYTES
+    x, xv = activations("bf16", synth.normal_rows(9, m, k))
+    got = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    jq.matmul_noalloc(gpu, x, m, w, got)
+    whole = torch.empty_like(got)
+    jq.matmul_plan(gpu, x, m, w, whole, None, jq.Plan(plan.bm, plan.bn, 1))
+    split = torch.empty_like(got)
+    jq.matmul(gpu, x, m, w, split, None)  # no scratch given: the context's own holds the partials
+    torch.cuda.synchronize()
+    assert torch.equal(got, whole)
+    ref = torch.empty_like(got)
+    jq.matmul_plan(gpu, x, m, w, ref, jq.SplitScratch(gpu), plan)
+    assert torch.equal(split, ref)
+    scale = whole.abs().max().item()
+    assert (split - whole).abs().max().item() <= 1e-4 * scale
+
