@@ -388,8 +388,8 @@ def measure_configs(gpu, steps):
                           "weight_GBps": round(raw.size / (t * 1e-3) / 1e9, 1),
                           "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                                        "unit": "TFLOP/s", "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}}
-    # decode-time expert product: 8 tokens routed to 8 of the 128 experts each (64 assignments,
-    # one or two rows per touched expert) on the small-row grouped path (jobs of up to 2 rows),
+    # decode-time expert product: 8 tokens routed to 8 of the 128 experts each (64 assignments)
+    # on the small-row grouped path in jobs of up to 4 rows (SMALL_GROUP_ROWS, model.rs:265),
     # timed over weight copies that together exceed the last-level cache
     tokens_d = 8
     route_d = np.stack([rng.choice(experts, top_k, replace=False) for _ in range(tokens_d)]).reshape(-1)
@@ -402,13 +402,13 @@ def measure_configs(gpu, steps):
     ids_d = torch.from_numpy(route_d.astype(np.int32)).cuda()
     xd = xrows(tokens_d, k, 9)
     outd = torch.empty((tokens_d * top_k, n), dtype=torch.float32, device="cuda")
-    gd = jq.group_routes(gpu, ids_d, experts, 2, in_div=top_k)
-    jq.matvec_grouped(gpu, xd, w, gd, outd, 2)
-    t = kernel_time_ms(lambda r: jq.matvec_grouped(gpu, xd, wd[r % copies], gd, outd, 2), max(4, steps // 10))
+    gd = jq.group_routes(gpu, ids_d, experts, 4, in_div=top_k)
+    jq.matvec_grouped(gpu, xd, w, gd, outd, 4)
+    t = kernel_time_ms(lambda r: jq.matvec_grouped(gpu, xd, wd[r % copies], gd, outd, 4), max(4, steps // 10))
     gbs = tbytes / (t * 1e-3) / 1e9
     res["moe_grouped_decode"] = {"workload": f"Q4_K expert-grouped small-row product, {experts} experts N={n} K={k}, "
                                              f"{tokens_d} tokens x top-{top_k} ({touched} experts touched), "
-                                             "jobs of up to 2 rows, bf16 activations, f32 out",
+                                             "jobs of up to 4 rows, bf16 activations, f32 out",
                                  "kernel_us": round(t * 1e3, 2), "weight_bytes_touched": tbytes,
                                  "rotation_copies": copies,
                                  "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
@@ -420,35 +420,54 @@ def measure_configs(gpu, steps):
 
 
 def cpu_baseline(raw, n, k, x32):
-    import oracle as O
-
-    threads = O.omp_max_threads()
+    """The oracle's port of the reference CPU path on this host's cores: GGML block decode
+    (quant.rs:83-101) then an f32-accumulate matmul (OpenMP over all cores). Main figure: the
+    Q4_K matrix at M = 1, decode + matmul, about 10 s of repetitions; beside it the matmul alone
+    on pre-decoded f32 weights, one thread on 1024 rows, and the Q8_0 GEMV (M = 1, K = N = 4096,
+    f32 activations) decode + matmul, about 3 s each."""
     import numpy as np
 
+    import oracle as O
+    from jevons_qmm import synth
+
+    threads = O.omp_max_threads()
     wdec = np.empty(n * k, np.float32)
     nbytes = n * k // 256 * 144
-    O.cpu_dequant_matmul(O.Q4K, raw, n, k, x32[:1], threads=threads, wdec=wdec)  # warm
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < 10.0:
-        O.cpu_dequant_matmul(O.Q4K, raw, n, k, x32[:1], threads=threads, wdec=wdec)
-        reps += 1
-    dt = (time.perf_counter() - t0) / reps
+
+    def timed(fn, seconds):
+        fn()  # warm
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            fn()
+            reps += 1
+        return (time.perf_counter() - t0) / reps, reps
+
+    dt, reps = timed(lambda: O.cpu_dequant_matmul(O.Q4K, raw, n, k, x32[:1], threads=threads, wdec=wdec), 10.0)
+    # the matmul alone: wdec holds the decoded weights from the runs above
+    dm, reps_m = timed(lambda: O.cpu_dequant_matmul(O.Q4K, raw, n, k, x32[:1], threads=threads, wdec=wdec,
+                                                    decode=False), 3.0)
     # single thread on a 1024-row slice of the same matrix
     rows1 = 1024
     raw1 = raw[: rows1 * k // 256 * 144]
-    t1 = time.perf_counter()
-    reps1 = 0
-    while time.perf_counter() - t1 < 3.0:
-        O.cpu_dequant_matmul(O.Q4K, raw1, rows1, k, x32[:1], threads=1, wdec=wdec)
-        reps1 += 1
-    dt1 = (time.perf_counter() - t1) / reps1
+    d1, _ = timed(lambda: O.cpu_dequant_matmul(O.Q4K, raw1, rows1, k, x32[:1], threads=1, wdec=wdec), 3.0)
+    # Q8_0 GEMV M = 1, K = N = 4096, f32 activations
+    n8 = k8 = 4096
+    raw8 = synth.weights(O.Q8_0, 3, n8, k8)
+    x8 = synth.normal_rows(1, 1, k8)
+    w8 = np.empty(n8 * k8, np.float32)
+    d8, reps8 = timed(lambda: O.cpu_dequant_matmul(O.Q8_0, raw8, n8, k8, x8, threads=threads, wdec=w8), 3.0)
     return {
         "value": round(nbytes / dt / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"Q4_K decode + f32 matmul, M=1, K={k}, N={n} (full matrix), {reps} reps in ~10 s; "
-                  f"1 thread on 1024 rows: {round(rows1 * k // 256 * 144 / dt1 / 1e9, 3)} GB/s",
+        "sample": f"Q4_K decode + f32 matmul, M=1, K={k}, N={n} (full matrix), {reps} reps in ~10 s",
+        "ms_per_call": round(dt * 1e3, 3),
+        "matmul_only_predecoded": {"ms_per_call": round(dm * 1e3, 3), "q4k_weight_GBps": round(nbytes / dm / 1e9, 3),
+                                   "f32_weight_GBps": round(n * k * 4 / dm / 1e9, 3), "reps": reps_m},
+        "one_thread_1024_rows": {"q4k_weight_GBps": round(rows1 * k // 256 * 144 / d1 / 1e9, 3)},
+        "q8_0_gemv_4096": {"ms_per_call": round(d8 * 1e3, 3), "weight_GBps": round(raw8.size / d8 / 1e9, 3),
+                           "reps": reps8, "cores": threads},
         "cpu_model": _cpu_model(),
     }
 

@@ -1241,11 +1241,12 @@ jv_status jv_matvec_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len
     if (mr == 0 || mr > 16) return fail(JV_ERR_INVALID, "matvec_grouped handles 1 to 16 rows per job");
     if (g->rows == 0 || g->max_jobs == 0) return JV_OK;
     // Q4_K, Q6_K and Q8_0 jobs run the small-row per-tile kernel in grouped mode (grid y = job),
-    // which streams each job's expert weights as the decode GEMV does; its LDS holds mr rows.
-    // Jobs of more than 2 rows go through in chunks of 2, so the LDS holds at most 2 rows
-    // (8 tokens x top-8 at mr = 16: 37 us against 85 us on the generic tiles).
-    // 128 experts [1408, 2816], 8 tokens x top-8: 32 us at mr = 2 (3.7 TB/s of touched expert
-    // weights) against 42 us on the generic grouped tiles. JV_QMVG=0 takes the generic tiles.
+    // which streams each job's expert weights as the decode GEMV does. Jobs of up to 8 rows go
+    // through in one pass (rows spread over the lane groups); larger ones in chunks of 2, so
+    // the LDS holds at most 8 rows. 128 experts [1408, 2816], 8 / 32 tokens x top-8: jobs of
+    // up to 4 rows (the reference's SMALL_GROUP_ROWS) 27 / 67 us against 46 / 84 us on the
+    // generic grouped tiles (and 31 / 87 us in 2-row chunks); mr = 16 30 / 81 us against 89 /
+    // 185 us. JV_QMVG=0 takes the generic tiles.
     const char *genv = getenv("JV_QMVG");
     if ((w->fmt == JV_FMT_Q4K || w->fmt == JV_FMT_Q6K || w->fmt == JV_FMT_Q8_0) &&
         w->n * w->experts * w->k < (1ull << 32) && !(genv && genv[0] == '0')) {
@@ -1258,7 +1259,7 @@ jv_status jv_matvec_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len
         // per wave, as the kernel computes it: FP16 activations [mv][ku umax + 8], sums
         // [mv][ku umax / xg], a zero row for Q6_K, mv range factors; at least the 1 KB of the
         // tile partial
-        const size_t mv = mr == 1 ? 1 : 2;  // rows per chunk
+        const size_t mv = mr <= 8 ? mr : 2;  // rows per pass
         const size_t row = ((size_t)umax * ku + 8) * 2;
         const size_t stage = (mv * row + mv * umax * (ku / xg) * 4 + (q6 ? row : 0) + mv * 4 + 15) & ~(size_t)15;
         const size_t lds = std::max(stage, (size_t)1024) * waves;
@@ -1284,7 +1285,7 @@ jv_status jv_matvec_grouped(jv_ctx *ctx, const void *x, jv_act act, size_t x_len
             void *args[] = {&p};
             char name[32];
             snprintf(name, sizeof name, "jv_qmvg_%s_%s", q8 ? "q8_0" : (q6 ? "q6k" : "q4k"),
-                     mr == 1 ? "m1" : (mr == 2 ? "m2" : "c2"));
+                     mr <= 4 ? "m1" : (mr <= 8 ? "m2" : "c2"));
             return launch(ctx, name, dim3((unsigned)(w->n / 16), (unsigned)g->max_jobs), dim3(64 * waves),
                           lds, stream, args);
         }

@@ -1627,11 +1627,11 @@ JV_QMV8(2, 4, 8)
 // Expert-grouped small-row kernels (matvec_grouped, gemm.rs:1171-1203): grid y is the job, one
 // 16-row weight tile of the job's expert per workgroup; the job's rows (at most rows_cap) are
 // its sorted positions, read from input rows ids[s] / in_div and written to output rows
-// ids[s]. Unused job slots return before any barrier. Jobs of more than 2 rows go through in
-// chunks of 2 rows (_c2), a barrier between chunks (the next chunk's staging reuses the LDS the
-// partials were read from), so the LDS holds 2 rows whatever rows_cap is; a later chunk reads
-// the tile again, from L2. Jobs of 1 or 2 rows take the single-pass kernels (_m1, _m2), which
-// need fewer registers.
+// ids[s]. Unused job slots return before any barrier. Jobs of up to 4 rows take the one-pass
+// kernel _m1 (rows spread one per lane group), up to 8 rows _m2 (two per group). Larger jobs
+// go through in chunks of 2 rows (_c2), a barrier between chunks (the next chunk's staging
+// reuses the LDS the partials were read from), so the LDS holds 2 rows whatever rows_cap is;
+// a later chunk reads the tile again, from L2. Every variant gives the same bits.
 #define JV_QMVG_HEAD                                                                          \
     const int job = blockIdx.y;                                                               \
     if (job >= (int)p.jobs[0]) return;                                                        \
@@ -1647,7 +1647,7 @@ JV_QMV8(2, 4, 8)
         q.ids = p.ids + js;                                                                   \
         qmv_body<G, W, 1, P, MV, XB, true>(q, (int)e * (p.N >> 4));                           \
     }
-// jobs of more rows: chunks of 2
+// jobs of more rows: chunks of 2 rows
 #define JV_QMVGC(NAME, G, W, P)                                                               \
     extern "C" __global__ __launch_bounds__(64 * W) void jv_qmvg_##NAME##_c2(QmmParams p) {   \
         JV_QMVG_HEAD                                                                          \

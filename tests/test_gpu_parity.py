@@ -663,7 +663,8 @@ def test_small_row_grouped_products(gpu, monkeypatch, name, type_id):
     """matvec_grouped on the small-row kernels in grouped mode (grid y = job; rows gathered from
     ids / in_div, the expert's weight tiles, output rows scattered to ids): jobs of 1, 2, 4 and
     16 rows, uneven expert loads with an empty expert, K of several items per wave, f32 and
-    bf16 outputs, against the f64 oracle and the generic grouped tiles (JV_QMVG=0)."""
+    bf16 outputs, against the f64 oracle and the generic grouped tiles (JV_QMVG=0); every job
+    size gives each assignment's row the same bits."""
     experts, n, k, top_k, tokens = 8, 192, 3840 if type_id != jq.Q8_0 else 4096, 2, 21
     raw = synth.weights(type_id, 81, experts * n, k)
     w = jq.QMatrix.upload(gpu, type_id, n, k, experts, raw)
@@ -672,7 +673,8 @@ def test_small_row_grouped_products(gpu, monkeypatch, name, type_id):
     rng = np.random.default_rng(83)
     ids = rng.choice([0, 1, 1, 2, 3, 3, 3, 5, 6, 7], tokens * top_k).astype(np.uint32)  # expert 4 empty
     want = O.grouped_product_f64(xv, dense, ids, top_k, n)
-    for mr in (1, 2, 4, 16):
+    first = None
+    for mr in (1, 2, 4, 5, 8, 16):
         g = jq.group_routes(gpu, _i32(ids), experts, mr, in_div=top_k)
         outs = {}
         for flag in ("1", "0"):
@@ -681,10 +683,42 @@ def test_small_row_grouped_products(gpu, monkeypatch, name, type_id):
             jq.matvec_grouped(gpu, x, w, g, out, mr)
             outs[flag] = out.cpu().numpy()
             assert err(outs[flag], want) <= TOL, (mr, flag)
+        # one-pass jobs of 1-4 and 5-8 rows and 2-row chunks: the same bits for every job size
+        if first is None:
+            first = outs["1"]
+        assert np.array_equal(outs["1"], first), mr
         monkeypatch.setenv("JV_QMVG", "1")
         o16 = torch.zeros((ids.size, n), dtype=torch.bfloat16, device="cuda")
         jq.matvec_grouped(gpu, x, w, g, o16, mr)
         assert err(o16.float().cpu().numpy(), want) <= 8e-3, mr
+
+
+@pytest.mark.parametrize("name,type_id,k", [("q4k", jq.Q4K, 256), ("q6k", jq.Q6K, 256), ("q8_0", jq.Q8_0, 512),
+                                            ("q4k", jq.Q4K, 2816), ("q6k", jq.Q6K, 1536)])
+@pytest.mark.parametrize("act", ["f16", "f32"])
+def test_small_row_grouped_products_other_inputs(gpu, monkeypatch, name, type_id, k, act):
+    """matvec_grouped as the reference calls it for the down projection (model.rs:968): each
+    assignment's own input row (in_div = 1), with f16 activations, and with f32 activations
+    through the grouped staging; K = 256 leaves 3 of the 4 waves of the Q4_K / Q6_K grouped
+    kernels without items. Jobs of 1, 2, 4 and 16 rows against the f64 oracle."""
+    experts, n, top_k, tokens = 8, 128, 2, 13
+    raw = synth.weights(type_id, 91, experts * n, k)
+    w = jq.QMatrix.upload(gpu, type_id, n, k, experts, raw)
+    dense = O.dequantize(type_id, raw).reshape(experts * n, k)
+    rng = np.random.default_rng(92)
+    ids = rng.choice([0, 1, 1, 2, 3, 3, 3, 5, 6, 7], tokens * top_k).astype(np.uint32)  # expert 4 empty
+    x, xv = activations(act, synth.normal_rows(93, tokens * top_k, k))
+    if act == "f32":
+        xv = xv.astype(np.float16).astype(np.float32)  # the kernels stage FP16 activations
+    want = O.grouped_product_f64(xv, dense, ids, 1, n)
+    monkeypatch.setenv("JV_QMVG", "1")
+    for mr in (1, 2, 4, 16):
+        g = jq.group_routes(gpu, _i32(ids), experts, mr, in_div=1)
+        out = torch.full((ids.size, n), float("nan"), dtype=torch.float32, device="cuda")
+        jq.matvec_grouped(gpu, x, w, g, out, mr)
+        e = err(out.cpu().numpy(), want)
+        say(name, act, "k", k, "mr", mr, "normalized error", e)
+        assert e <= TOL, (mr, e)
 
 
 @pytest.mark.parametrize("name,type_id", [("q4k", jq.Q4K), ("q6k", jq.Q6K), ("q8_0", jq.Q8_0), ("q5_0", jq.Q5_0)])
