@@ -804,6 +804,48 @@ def test_argmax_random_rows_with_ties(gpu, n):
     assert jq.argmax_rows(gpu, shifted, s).cpu().tolist() == want
 
 
+def test_argmax_repeats_and_graph_replays(gpu):
+    """The argmax's partials live in the scratch buffer: consecutive calls on new logits, calls
+    interleaved with a split-K small-row product on the same scratch (tile counters and
+    partials), and replays of a captured graph with eager work between them all give greedy's
+    answers."""
+    s = jq.SplitScratch(gpu)
+    rng = np.random.default_rng(5)
+    rows, n = 8, 262144
+
+    def fresh():
+        host = rng.integers(-50, 50, size=(rows, n)).astype(np.float32)
+        host[3, rng.integers(0, n)] = np.nan
+        return host
+
+    w = jq.QMatrix.upload(gpu, jq.Q4K, 256, 15360, 1, synth.weights(jq.Q4K, 6, 256, 15360))
+    x, _ = activations("bf16", synth.normal_rows(7, 16, 15360))
+    out = torch.empty((16, 256), dtype=torch.float32, device="cuda")
+    for i in range(4):
+        host = fresh()
+        got = jq.argmax_rows(gpu, torch.from_numpy(host).cuda(), s).cpu().tolist()
+        assert got == [_greedy_or_minus_one(r) for r in host], i
+        jq.matmul(gpu, x, 16, w, out, s)  # split-K small-row kernel (K = 15360, m = 16)
+    t = torch.from_numpy(fresh()).cuda()
+    jq.argmax_rows(gpu, t, s)  # buffers grow before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(g, stream=st):
+            idx = jq.argmax_rows(gpu, t, s)
+    torch.cuda.current_stream().wait_stream(st)
+    for i in range(3):
+        host = fresh()
+        t.copy_(torch.from_numpy(host))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert idx.cpu().tolist() == [_greedy_or_minus_one(r) for r in host], i
+        jq.matmul(gpu, x, 16, w, out, s)
+
+
 @pytest.mark.parametrize("m", [1, 8, 32])
 def test_q6k_lm_head_logits_and_argmax(gpu, m):
     """Q6_K vocabulary projection K=3840 on 16384 rows of the vocabulary: logits against the f64
