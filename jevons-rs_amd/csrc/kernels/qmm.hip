@@ -905,6 +905,18 @@ __device__ __forceinline__ int spread_out(int g, int i, int rpg, int M) {
     return i < rpg && m < M ? m : -1;
 }
 
+// Formats whose scale groups are 16 columns (Q6_K) run each 32-k step as MFMA rows of activation
+// rows masked to one half of the step: MFMA row 4q + 2a + h reads activation row q rpg + a (the
+// row of accumulator element a of lane group q) in lane groups 2h, 2h + 1 and the zero row in
+// the others, so the element of row 4q + 2a + h is the half-h sum of that row. Up to 8 rows (two
+// per lane group) fit one MFMA. The lane's A pointer for that layout:
+__device__ __forceinline__ const _Float16 *half_row(const _Float16 *xs, const _Float16 *zrow, int stride,
+                                                  int r, int g, int M) {
+    const int rpg = (M + 3) >> 2;
+    const int row = min((r >> 2) * rpg + min((r >> 1) & 1, rpg - 1), M - 1);
+    return ((g >> 1) == (r & 1)) ? xs + row * stride : zrow;
+}
+
 // Multiplies a lane's accumulator (lane group g's rows) by the rows' range factors.
 __device__ __forceinline__ void unscale_rows(f32x4 &a, const float *Sc, int g, int M) {
     const int rpg = (M + 3) >> 2;
@@ -1148,7 +1160,7 @@ struct GQ6K {
         it.dv = *(const uint16_t *)(tb + 3328u + (uint32_t)(2 * r));
     }
     template <int MV>
-    __device__ static void block(const Item &it, const _Float16 *xrow, const _Float16 *zrow,
+    __device__ static void block(const Item &it, const _Float16 *xrow, const _Float16 *xalt,
                                  const float *Xrow, int ul, int g, const Lane &c, f32x4 &acc) {
         const uint4 scw = q4k_head_gather(it.hv);  // the row's 16 scales, 4 per dword
         const uint32_t SC[4] = {scw.x, scw.y, scw.z, scw.w};
@@ -1158,8 +1170,10 @@ struct GQ6K {
         uint32_t magic = 0x64006400u;
         asm("" : "+v"(magic));
         const int kb = ul * 256 + 8 * g;
-        const _Float16 *xlo = (g < 2 ? xrow : zrow) + kb;
-        const _Float16 *xhi = (g < 2 ? zrow : xrow) + kb;
+        // MV <= 2: xalt is the lane's half_row pointer (both halves of a step in one MFMA);
+        // MV = 4: xalt is the zero row, and each step runs an MFMA per half
+        const _Float16 *xlo = (MV <= 2 ? xalt : (g < 2 ? xrow : xalt)) + kb;
+        const _Float16 *xhi = (g < 2 ? xalt : xrow) + kb;
         float v[MV];
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
@@ -1177,17 +1191,28 @@ struct GQ6K {
                 bq[2 * p2 + 1] = __builtin_amdgcn_perm(magic, q6, 0x05030501u);
             }
             const f16x8 bf = __builtin_bit_cast(f16x8, bq);
-            const f32x4 S0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xlo + 32 * s), bf,
-                                                                    f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            const f32x4 S1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xhi + 32 * s), bf,
-                                                                    f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
             const int t0 = 2 * s, t1 = 2 * s + 1;
             const float sc0 = (float)(int32_t)(int8_t)((SC[t0 >> 2] >> (8 * (t0 & 3))) & 0xffu);
             const float sc1 = (float)(int32_t)(int8_t)((SC[t1 >> 2] >> (8 * (t1 & 3))) & 0xffu);
+            if constexpr (MV <= 2) {
+                // element 2a + h: accumulator row a, half h
+                const f32x4 S = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xlo + 32 * s), bf,
+                                                                       f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-            for (int m = 0; m < MV; ++m) {
-                v[m] = s == 0 ? sc0 * S0[m] : __builtin_fmaf(sc0, S0[m], v[m]);
-                v[m] = __builtin_fmaf(sc1, S1[m], v[m]);
+                for (int m = 0; m < MV; ++m) {
+                    v[m] = s == 0 ? sc0 * S[2 * m] : __builtin_fmaf(sc0, S[2 * m], v[m]);
+                    v[m] = __builtin_fmaf(sc1, S[2 * m + 1], v[m]);
+                }
+            } else {
+                const f32x4 S0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xlo + 32 * s), bf,
+                                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                const f32x4 S1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xhi + 32 * s), bf,
+                                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+                for (int m = 0; m < MV; ++m) {
+                    v[m] = s == 0 ? sc0 * S0[m] : __builtin_fmaf(sc0, S0[m], v[m]);
+                    v[m] = __builtin_fmaf(sc1, S1[m], v[m]);
+                }
             }
         }
 #pragma unroll
@@ -1268,6 +1293,7 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p, int wt_off = 0) {
         const int arow = spread_row(r16, (p.M + 3) >> 2, p.M);
         const _Float16 *xrow = xs + arow * stride;
         const float *Xrow = Xs + arow * xstride;
+        const _Float16 *xalt = G::kZeroRow && MV <= 2 ? half_row(xs, zrow, stride, r16, g, p.M) : zrow;
         const typename G::Lane lc = G::lane_consts(g);
         for (int i0 = 0; i0 < nitems; i0 += P) {
 #pragma unroll
@@ -1279,7 +1305,7 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p, int wt_off = 0) {
 #pragma unroll
                     for (int t = 1; t < TW; ++t)
                         if (t == tw) a = acc[t];
-                    G::template block<MV>(buf[j], xrow, zrow, Xrow, idx - tw * nu, g, lc, a);
+                    G::template block<MV>(buf[j], xrow, xalt, Xrow, idx - tw * nu, g, lc, a);
 #pragma unroll
                     for (int t = 0; t < TW; ++t)
                         if (t == tw) acc[t] = a;
@@ -1420,6 +1446,7 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
         const int arow = spread_row(r16, (p.M + 3) >> 2, p.M);
         const _Float16 *xrow = xs + arow * stride;
         const float *Xrow = Xs + arow * xstride;
+        const _Float16 *xalt = G::kZeroRow && MV <= 2 ? half_row(xs, zrow, stride, r16, g, p.M) : zrow;
         const typename G::Lane lc = G::lane_consts(g);
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         int ul = 0;
@@ -1427,7 +1454,7 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
 #pragma unroll
             for (int j = 0; j < P; ++j) {
                 if (i0 + j < nitems) {
-                    G::template block<MV>(buf[j], xrow, zrow, Xrow, ul, g, lc, acc);
+                    G::template block<MV>(buf[j], xrow, xalt, Xrow, ul, g, lc, acc);
                     if (++ul == nu) {
                         end_tile(acc);
                         acc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1520,12 +1547,13 @@ __device__ __forceinline__ void qmvs_body(const QmmParams &p) {
             const int arow = spread_row(r16, (p.M + 3) >> 2, p.M);
             const _Float16 *xrow = xs + arow * stride;
             const float *Xrow = Xs + arow * xstride;
+            const _Float16 *xalt = G::kZeroRow && MV <= 2 ? half_row(xs, zrow, stride, r16, g, p.M) : zrow;
             const typename G::Lane lc = G::lane_consts(g);
             for (int i0 = 0; i0 < nu; i0 += P) {
 #pragma unroll
                 for (int j = 0; j < P; ++j) {
                     const int idx = i0 + j;
-                    if (idx < nu) G::template block<MV>(buf[j], xrow, zrow, Xrow, idx, g, lc, acc);
+                    if (idx < nu) G::template block<MV>(buf[j], xrow, xalt, Xrow, idx, g, lc, acc);
                     if (i0 + P < nu) load_item(buf[j], idx + P);
                 }
             }
