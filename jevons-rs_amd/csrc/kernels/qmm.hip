@@ -1131,13 +1131,14 @@ struct GQ8_0 {
 };
 
 // Q6_K as a small-row format: item = one 256-element block of a 16-row tile. Step s (32 k,
-// lane group g holding k = 32s + 8g + e) builds the exact FP16 operands 1024 + q6 from the low
-// nibble and the two high bits, and runs two MFMAs on them: one with the activations of lane
-// groups 0, 1 (scale group 2s) and one with those of groups 2, 3 (group 2s + 1), the other
-// half reading a zero row. Then out += d sum_t sc_t S_t - sum_t 1056 d sc_t X_t (1056 = 1024
-// + the 32 offset of quant.rs:43-61's q - 32), the second sum as four FP32 MFMAs 16x16x4 over
-// the 16-column activation sums (k index g: group 4j + g).
+// lane group g holding k = 32s + 8g + e) builds the FP16 operands 1024 + q6 from the low nibble
+// and the two high bits, then q6 - 32 (quant.rs:43-61's signed quant) with one packed FP16
+// subtraction of 1056, exact. The step's two 16-column scale groups (lane groups 0, 1: group
+// 2s; groups 2, 3: group 2s + 1) come out of one MFMA for up to 8 rows (half_row), or of two
+// MFMAs whose activations are masked to one half by a zero row. Then out += d sum_t sc_t S_t:
+// the products x (q6 - 32) are exact, so no activation sums or bias terms are needed.
 struct GQ6K {
+    static constexpr _Float16 kQ6Off = (_Float16)-1056.0f;
     static constexpr int KU = 256;
     static constexpr int XG = 16;
     static constexpr bool kZeroRow = true;
@@ -1190,7 +1191,9 @@ struct GQ6K {
                 bq[2 * p2] = __builtin_amdgcn_perm(magic, q6, 0x05020500u);
                 bq[2 * p2 + 1] = __builtin_amdgcn_perm(magic, q6, 0x05030501u);
             }
-            const f16x8 bf = __builtin_bit_cast(f16x8, bq);
+            // 1024 + q6 - 1056 = q6 - 32, the signed quant, exact in FP16
+            f16x8 bf = __builtin_bit_cast(f16x8, bq);
+            bf = bf + f16x8{kQ6Off, kQ6Off, kQ6Off, kQ6Off, kQ6Off, kQ6Off, kQ6Off, kQ6Off};
             const int t0 = 2 * s, t1 = 2 * s + 1;
             const float sc0 = (float)(int32_t)(int8_t)((SC[t0 >> 2] >> (8 * (t0 & 3))) & 0xffu);
             const float sc1 = (float)(int32_t)(int8_t)((SC[t1 >> 2] >> (8 * (t1 & 3))) & 0xffu);
@@ -1217,12 +1220,6 @@ struct GQ6K {
         }
 #pragma unroll
         for (int m = 0; m < MV; ++m) acc[m] = __builtin_fmaf(d, v[m], acc[m]);
-        const float kd = -1056.f * d;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float sc = (float)(int32_t)(int8_t)((SC[j] >> c.sh) & 0xffu);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[ul * 16 + 4 * j + g], kd * sc, acc, 0, 0, 0);
-        }
     }
 };
 
