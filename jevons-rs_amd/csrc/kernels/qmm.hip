@@ -1081,10 +1081,11 @@ struct GQ4K {
 };
 
 // Q8_0 as a small-row format: item = 64 k (two blocks) of a 16-row tile. Block b is one MFMA on
-// the exact FP16 operands 1152 + q (0x6400 | (q + 128), the stored byte), scaled by d_b; the
-// 1152 X_b terms come from one FP32 MFMA 16x16x4 with lane groups 0, 1 holding blocks 0, 1
-// and groups 2, 3 zeros. This equals quant.rs:75-80's weights times x up to FP32 rounding.
+// the FP16 operands q: 0x6400 | (q + 128) (the stored byte) is 1152 + q, and one packed FP16
+// subtraction of 1152 leaves q exactly; the sum is scaled by d_b. The products x q are exact,
+// so this equals quant.rs:75-80's weights times x up to FP32 rounding, with no bias term.
 struct GQ8_0 {
+    static constexpr _Float16 kOff = (_Float16)-1152.0f;
     static constexpr int KU = 64;
     static constexpr int XG = 32;
     static constexpr bool kZeroRow = false;
@@ -1116,8 +1117,10 @@ struct GQ8_0 {
             bq.y = __builtin_amdgcn_perm(magic, w[2 * b], 0x05030501u);
             bq.z = __builtin_amdgcn_perm(magic, w[2 * b + 1], 0x05020500u);
             bq.w = __builtin_amdgcn_perm(magic, w[2 * b + 1], 0x05030501u);
-            S[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xrow + ul * 64 + 32 * b + 8 * g),
-                                                          __builtin_bit_cast(f16x8, bq),
+            // 1152 + q - 1152 = q, the signed quant, exact in FP16
+            f16x8 bf = __builtin_bit_cast(f16x8, bq);
+            bf = bf + f16x8{kOff, kOff, kOff, kOff, kOff, kOff, kOff, kOff};
+            S[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8 *)(xrow + ul * 64 + 32 * b + 8 * g), bf,
                                                           f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         }
 #pragma unroll
@@ -1125,8 +1128,6 @@ struct GQ8_0 {
             acc[i] = __builtin_fmaf(d0, S[0][i], acc[i]);
             acc[i] = __builtin_fmaf(d1, S[1][i], acc[i]);
         }
-        const float cb = g >= 2 ? 0.f : -1152.f * (g ? d1 : d0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Xrow[ul * 2 + (g & 1)], cb, acc, 0, 0, 0);
     }
 };
 
