@@ -1830,18 +1830,20 @@ __device__ __forceinline__ int packed_source(const PackXParams &p, int R) {
     return r < min((int)(p.offsets[e + 1] - s0), p.rows_cap) ? (int)(p.ids[s0 + r] / (uint32_t)p.in_div) : -1;
 }
 
-// BF16 / FP32 rows, 4 per workgroup of 4 NW waves: thread t handles row t % 4 and its chunks
-// t / 4 + 64 NW i (8 values each), so a wave's store writes 4 consecutive rows' 16-byte pieces
-// side by side (64 bytes) for 16 chunks. NW = min(4, ceil(K / 2048)) keeps each thread at 8
-// chunks or fewer, held in registers between the row's maximum and its conversion.
+// BF16 / FP32 rows, P = p.rpw (1, 2 or 4) per workgroup of NW waves: thread t handles row t % P
+// and its chunks t / P + (64 NW / P) i (8 values each), so a wave's store writes P consecutive
+// rows' 16-byte pieces side by side for 64 / P chunks. The host picks P and NW so that each
+// thread holds 8 chunks or fewer in registers between the row's maximum and its conversion, and
+// small row counts still spread over many workgroups.
 template <int ACT>
 __device__ __forceinline__ void pack_rows(const PackXParams &p) {
     __shared__ float wmax[16][4];
     __shared__ int wnf[16][4];
-    const int nthreads = (int)blockDim.x;  // 256 NW
+    const int nthreads = (int)blockDim.x;  // 64 NW
     const int t = (int)threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int rr = t & 3, cl = t >> 2, tpr = nthreads >> 2;  // row of the group, chunk lane, per row
-    const int R = (int)blockIdx.x * 4 + rr;
+    const int P = p.rpw;
+    const int rr = t & (P - 1), cl = t / P, tpr = nthreads / P;  // row of the group, chunk lane, per row
+    const int R = (int)blockIdx.x * P + rr;
     const int rows_out = p.rowmajor ? p.M : p.mtiles * 16;
     const int xr = R < rows_out ? packed_source(p, R) : -2;
     const int chunks = p.K >> 3;
@@ -1881,14 +1883,13 @@ __device__ __forceinline__ void pack_rows(const PackXParams &p) {
             }
         }
     }
-    // the row's maximum over the lanes of its row (same t % 4) and then over the waves
+    // the row's maximum over the lanes of its row (same t % P) and then over the waves
     int inf = nf ? 1 : 0;
-#pragma unroll
-    for (int off = 4; off < 64; off <<= 1) {
+    for (int off = P; off < 64; off <<= 1) {
         mx = __builtin_fmaxf(mx, __shfl_xor(mx, off));
         inf |= __shfl_xor(inf, off);
     }
-    if (lane < 4) {
+    if (lane < P) {
         wmax[wave][rr] = mx;
         wnf[wave][rr] = inf;
     }

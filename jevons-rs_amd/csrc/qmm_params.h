@@ -56,6 +56,7 @@ struct PackXParams {
     int32_t M, K, ldx, act;
     int32_t mtiles;      // 16-row tiles packed (M rounded up to the product's row tile)
     int32_t rowmajor;
+    int32_t rpw;         // BF16 / FP32: rows per workgroup (1, 2 or 4)
     // Expert-grouped mode: m-tiles [j rows_cap / 16, (j + 1) rows_cap / 16) hold job j's rows,
     // input rows ids[s] / in_div for sorted positions s of the job (QmmParams' job format).
     const uint32_t *ids, *offsets, *jobs;
