@@ -358,11 +358,28 @@ def measure_configs(gpu, steps):
         jq.argmax_rows(gpu, out, scratch)
         t = kernel_time_ms(lambda r: jq.matmul(gpu, x, m, ms[0], out, scratch), max(4, steps // 10))
         ta = kernel_time_ms(lambda r: jq.argmax_rows(gpu, out, scratch), max(4, steps // 10))
+
+        def three_steps(r):  # the reference's order: product, soft cap, greedy per row
+            jq.matmul(gpu, x, m, ms[0], out, scratch)
+            jq.softcap_logits(gpu, out, 30.0)
+            jq.argmax_rows(gpu, out, scratch)
+
+        t3 = kernel_time_ms(three_steps, max(4, steps // 10))
+        tf = kernel_time_ms(lambda r: jq.matmul_argmax(gpu, x, m, ms[0], out, 30.0, scratch), max(4, steps // 10))
+        tf0 = kernel_time_ms(lambda r: jq.matmul_argmax(gpu, x, m, ms[0], out, 0.0, scratch), max(4, steps // 10))
         gbs = wbytes / (t * 1e-3) / 1e9
         lm[str(m)] = {"kernel_us": round(t * 1e3, 2), "weight_GBps": round(gbs, 1),
                       "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                       "tflops": round(2.0 * m * n * k / (t * 1e-3) / 1e12, 1),
-                      "argmax_us": round(ta * 1e3, 2)}
+                      "argmax_us": round(ta * 1e3, 2),
+                      # greedy fused into the product (jv_matmul_argmax, no soft cap), less the
+                      # product alone
+                      "fused_argmax_us": round((tf0 - t) * 1e3, 2),
+                      # soft cap 30 and greedy after the product: as three launches, and fused
+                      # into the product (jv_matmul_argmax), each less the product alone
+                      "softcap_argmax_us": round((t3 - t) * 1e3, 2),
+                      "fused_softcap_argmax_us": round((tf - t) * 1e3, 2),
+                      "fused_total_us": round(tf * 1e3, 2)}
     del ms
     res["q6k_lm_head"] = {"workload": f"Q6_K vocabulary projection K={k} N={n} + per-row argmax, bf16 activations, f32 logits",
                           "weight_bytes": wbytes, "per_m": lm}

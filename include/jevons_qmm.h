@@ -220,6 +220,19 @@ jv_status jv_f16_matmul(jv_ctx *ctx, const void *x, size_t m, size_t k, const vo
 jv_status jv_argmax_rows(jv_ctx *ctx, const float *logits, size_t rows, size_t n,
                          int32_t *index, jv_scratch *scratch, void *stream);
 
+/* The vocabulary projection with its soft cap and greedy's argmax in one call (the full-logits
+ * forward, crates/jevons-gemma4-diffusion/src/model.rs:1192-1204: matmul, then softcap_logits;
+ * then greedy per row, crates/jevons-core/src/model.rs:180-187, :207-219): out [m, n] FP32 =
+ * x . W^T on jv_matmul's plan, soft-capped in place when cap > 0 (cap = 0: raw logits), and
+ * index[r] (device, m int32) = greedy's argmax of out row r (-1 for a row holding a non-finite
+ * value). The results equal jv_matmul, jv_softcap_logits and jv_argmax_rows in turn. The
+ * small-row and 32-row kernels soft-cap their outputs and leave each workgroup's per-row
+ * maximum in `scratch` as they store, so the logits are not read again; other plans run the
+ * three steps. m <= 65535. */
+jv_status jv_matmul_argmax(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                           const jv_qmatrix *w, float *out, size_t out_len, float cap, int32_t *index,
+                           jv_scratch *scratch, void *stream);
+
 /* Final-logit soft capping in place (softcap_logits, crates/jevons-gemma4-diffusion/src/gpu/
  * ops.rs:1159-1168, kernel :750-758): x[i] = cap * tanh(x[i] / cap) for i < len; cap > 0. */
 jv_status jv_softcap_logits(jv_ctx *ctx, float *x, size_t len, float cap, void *stream);

@@ -384,6 +384,26 @@ struct GroupArgs {
     uint32_t cap;
 };
 
+// The greedy epilogue asked of a product (jv_matmul_argmax): the soft cap and the scratch buffer
+// for the per-workgroup partials; the launch fills in where it put them and over how many
+// workgroup columns, or leaves `fused` false when the kernel it took has no such epilogue.
+struct GreedyArgs {
+    float cap = 0.f;
+    jv_scratch *scratch = nullptr;
+    float *val = nullptr;
+    int32_t *idx = nullptr;
+    int slots = 0;
+    bool fused = false;
+};
+
+// Records the partials of `rows` x `slots` workgroup columns at `payload` (values, then indices).
+void greedy_partials(GreedyArgs *gr, size_t rows, int slots, void *payload) {
+    gr->val = (float *)payload;
+    gr->idx = (int32_t *)((uint8_t *)payload + rows * (size_t)slots * 4);
+    gr->slots = slots;
+    gr->fused = true;
+}
+
 // Staging buffers of one product: `pack_bytes` of packed or converted activations (the context's
 // buffer, grown as needed) and `part_bytes` of split-K partials (after the counters of
 // `scratch`). With the fixed array of jv_matmul_noalloc both come from that array, one after
@@ -575,17 +595,24 @@ bool pipelined_plan(const jv_qmatrix *w, jv_plan plan) {
 // jv_matmul_noalloc, it also holds the packed activations in place of the context's buffer.
 jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, const jv_qmatrix *w,
                            void *out, jv_out out_type, jv_plan plan, void *stream,
-                           const GroupArgs *grp, jv_scratch *scratch = nullptr) {
+                           const GroupArgs *grp, jv_scratch *scratch = nullptr, GreedyArgs *gr = nullptr) {
     jv_status st = JV_OK;
     if (grp && plan.splits > 1) return fail(JV_ERR_INVALID, "grouped pipelined tiles do not split K");
     const int jobs_or_tiles = grp ? (int)grp->max_jobs : (int)((m + plan.bm - 1) / plan.bm);
     const int mtiles = jobs_or_tiles * (int)(plan.bm / 16);
+    // the greedy epilogue exists on the 32 x 64 register tiles (ungrouped, whole K, FP32 out)
+    const bool greedy = gr && !grp && plan.splits == 1 && plan.bm == 32 && plan.bn == 64 &&
+                        reg_format(w) && out_type == JV_OUT_F32;
+    const int slots = (int)(w->n / plan.bn);
     // fragments, then each packed row's range factor
     const size_t frag_bytes = (size_t)mtiles * 16 * w->k * 2;
-    const size_t part_bytes = plan.splits > 1 ? (size_t)plan.splits * m * w->n * 4 : 0;
+    const size_t part_bytes = plan.splits > 1 ? (size_t)plan.splits * m * w->n * 4
+                                              : (greedy ? m * (size_t)slots * 8 : 0);
     void *pack = nullptr, *partials = nullptr;
-    st = stage_buffers(ctx, scratch, frag_bytes + (size_t)mtiles * 16 * 4, part_bytes, &pack, &partials);
+    st = stage_buffers(ctx, greedy ? gr->scratch : scratch, frag_bytes + (size_t)mtiles * 16 * 4, part_bytes,
+                       &pack, &partials);
     if (st != JV_OK) return st;
+    if (greedy) greedy_partials(gr, m, slots, partials);
     float *rscale = (float *)((uint8_t *)pack + frag_bytes);
     st = launch_pack(ctx, x, act, m, w->k, mtiles, 0, (uint16_t *)pack, rscale, grp, plan.bm, stream);
     if (st != JV_OK) return st;
@@ -602,7 +629,13 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     gp.ldo = (int32_t)(w->n);
     gp.out_type = (int32_t)out_type;
     gp.splits = (int32_t)plan.splits;
-    gp.part = (float *)partials;
+    if (greedy) {
+        gp.cap = gr->cap;
+        gp.amax_val = gr->val;
+        gp.amax_idx = gr->idx;
+    } else {
+        gp.part = (float *)partials;
+    }
     gp.split_stride = (int64_t)(m * w->n);
     if (grp) {
         gp.ids = grp->ids;
@@ -621,8 +654,8 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     // Ungrouped 64 x 64 products run the 8-wave tile (two waves per SIMD); expert jobs keep the
     // 4-wave one, faster there.
     const bool w8 = reg && !grp && plan.bm == 64;
-    snprintf(name, sizeof name, "jv_gemm_%s_%ux%u%s", fmt_kernel_name(w->fmt), plan.bm, plan.bn,
-             w8 ? "r8" : (reg ? "r" : ""));
+    snprintf(name, sizeof name, "jv_gemm_%s_%ux%u%s%s", fmt_kernel_name(w->fmt), plan.bm, plan.bn,
+             w8 ? "r8" : (reg ? "r" : ""), greedy ? "_g" : "");
     const unsigned waves = plan.bm >= 128 || w8 ? 8 : 4;
     const size_t glds = 4 * ((reg ? 0 : plan.bm) + plan.bn) / 16 * 1024;
     st = launch(ctx, name, dim3((unsigned)(w->n / plan.bn), (unsigned)jobs_or_tiles, plan.splits),
@@ -638,7 +671,7 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
 
 jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
                       const jv_qmatrix *w, void *out, jv_out out_type, size_t out_len,
-                      jv_plan plan, jv_scratch *scratch, void *stream) {
+                      jv_plan plan, jv_scratch *scratch, void *stream, GreedyArgs *gr = nullptr) {
     jv_status st = use_device(ctx);
     if (st != JV_OK) return st;
     if (!w) return fail(JV_ERR_INVALID, "null weight matrix");
@@ -742,13 +775,24 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
                               args);
             }
             if (persist) {
-                snprintf(name, sizeof name, "jv_qmvp_%s_m%d", fname, mv);
+                // the greedy epilogue: FP32 outputs, a variant of the same kernel
+                const bool greedy = gr && out_type == JV_OUT_F32;
+                snprintf(name, sizeof name, "jv_qmvp_%s_m%d%s", fname, mv, greedy ? "_g" : "");
                 hipFunction_t f;
                 st = get_fn(ctx, name, &f);
                 if (st != JV_OK) return st;
                 int per_cu = 0;
                 JV_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 64 * waves, lds));
                 const int grid = std::min(T, cus * std::max(1, per_cu));
+                if (greedy) {
+                    void *payload = nullptr;
+                    st = scratch_reserve(gr->scratch, m * (size_t)grid * 8, &payload);
+                    if (st != JV_OK) return st;
+                    greedy_partials(gr, m, grid, payload);
+                    p.cap = gr->cap;
+                    p.amax_val = gr->val;
+                    p.amax_idx = gr->idx;
+                }
                 return launch(ctx, name, dim3((unsigned)grid), dim3(64 * waves), lds, stream, args);
             }
             snprintf(name, sizeof name, "jv_qmv_%s_t%d_m%d", fname, tw, mv);
@@ -756,7 +800,7 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         }
     }
     if (pipelined_plan(w, plan))
-        return launch_pipelined(ctx, x, act, m, w, out, out_type, plan, stream, nullptr, scratch);
+        return launch_pipelined(ctx, x, act, m, w, out, out_type, plan, stream, nullptr, scratch, gr);
     return launch_tiles(ctx, x, act, m, w, out, out_type, scratch, plan, stream, nullptr);
 }
 
@@ -1361,6 +1405,39 @@ jv_status jv_argmax_rows(jv_ctx *ctx, const float *logits, size_t rows, size_t n
     }
     void *a2[] = {&pval, &pidx, &chunks, &index};
     return launch(ctx, "jv_argmax_final", dim3((unsigned)rows), dim3(256), 0, stream, a2);
+}
+
+jv_status jv_matmul_argmax(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
+                           const jv_qmatrix *w, float *out, size_t out_len, float cap, int32_t *index,
+                           jv_scratch *scratch, void *stream) {
+    if (!ctx) return fail(JV_ERR_INVALID, "null context");
+    if (!w) return fail(JV_ERR_INVALID, "null weight matrix");
+    if (!(cap >= 0.f) || !std::isfinite(cap))
+        return fail(JV_ERR_INVALID, "softcap %g must be 0 (none) or positive", (double)cap);
+    if (!index) return fail(JV_ERR_INVALID, "null index buffer");
+    if (!scratch) return fail(JV_ERR_INVALID, "argmax needs a scratch buffer");
+    if (m > 65535 || w->n > (size_t)INT32_MAX)
+        return fail(JV_ERR_INVALID, "argmax of %zu rows x %zu is too large", m, w->n);
+    // jv_matmul's plan; its small-row persistent kernels and 32 x 64 tiles have a variant with
+    // the greedy epilogue, and any other kernel is followed by the soft cap and jv_argmax_rows
+    const jv_plan plan = jv_plan_auto(w, m, 0);
+    GreedyArgs gr;
+    gr.cap = cap;
+    gr.scratch = scratch;
+    jv_status st = run_product(ctx, x, act, x_len, m, w, out, JV_OUT_F32, out_len, plan, scratch, stream, &gr);
+    if (st != JV_OK || m == 0) return st;
+    if (gr.fused) {
+        float *pval = gr.val;
+        int32_t *pidx = gr.idx;
+        int chunks = gr.slots;
+        void *a2[] = {&pval, &pidx, &chunks, &index};
+        return launch(ctx, "jv_argmax_final", dim3((unsigned)m), dim3(256), 0, stream, a2);
+    }
+    if (cap > 0.f) {
+        st = jv_softcap_logits(ctx, out, m * w->n, cap, stream);
+        if (st != JV_OK) return st;
+    }
+    return jv_argmax_rows(ctx, out, m, w->n, index, scratch, stream);
 }
 
 jv_status jv_softcap_logits(jv_ctx *ctx, float *x, size_t len, float cap, void *stream) {

@@ -905,6 +905,56 @@ __device__ __forceinline__ int spread_out(int g, int i, int rpg, int M) {
     return i < rpg && m < M ? m : -1;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Greedy epilogue of the vocabulary projection (lm_head, soft cap and greedy fused:
+// crates/jevons-gemma4-diffusion/src/model.rs:1194-1204 and gpu/ops.rs:750-758, then
+// crates/jevons-core/src/model.rs:207-219 on each row): outputs are soft-capped before they are
+// stored, and each workgroup leaves per row the largest value of its columns and that value's
+// first column, for jv_argmax_final.
+// ---------------------------------------------------------------------------------------------
+// (v, i) replaces (bv, bi) if larger, or equal with a lower index: greedy's first maximum.
+__device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+// The soft cap of one output value, the same expression as jv_softcap's; cap 0 leaves it.
+__device__ __forceinline__ float soft_capped(float v, float cap) { return cap > 0.f ? cap * tanhf(v / cap) : v; }
+
+// Largest value, its first column and whether any value was not finite, over the columns of one
+// output row that a lane (then a lane group, a wave, a workgroup) stores.
+struct Greedy {
+    float v;
+    int i;
+    int bad;
+    __device__ static Greedy none() { return Greedy{-__builtin_inff(), 0x7fffffff, 0}; }
+    __device__ void add(float x, int col) {
+        bad |= !__builtin_isfinite(x);
+        better(v, i, x, col);
+    }
+    __device__ void merge(const Greedy &o) {
+        better(v, i, o.v, o.i);
+        bad |= o.bad;
+    }
+    // over the 16 lanes of the lane group (the lanes that hold the same output rows)
+    __device__ void group16() {
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+            const float ov = __shfl_xor(v, off);
+            const int oi = __shfl_xor(i, off);
+            const int ob = __shfl_xor(bad, off);
+            better(v, i, ov, oi);
+            bad |= ob;
+        }
+    }
+    __device__ void write(float *val, int32_t *idx, size_t o) const {
+        val[o] = v;
+        idx[o] = bad ? -1 : i;
+    }
+};
+
 // Formats whose scale groups are 16 columns (Q6_K) run each 32-k step as MFMA rows of activation
 // rows masked to one half of the step: MFMA row 4q + 2a + h reads activation row q rpg + a (the
 // row of accumulator element a of lane group q) in lane groups 2h, 2h + 1 and the zero row in
@@ -1351,7 +1401,9 @@ __device__ __forceinline__ void qmv_body(const QmmParams &p, int wt_off = 0) {
 // writes its partial of every tile to an LDS slot; after every TS tiles one barrier, then wave t
 // adds tile t's W partials in wave order (slots double-buffered, so the next chunk's partials
 // never overwrite ones still being added). Every output element is the same sum as in qmv_body.
-template <class G, int W, int TS, int P, int MV, int XB>
+// GR: the greedy epilogue (FP32 outputs soft-capped, per-row partial argmax of the workgroup's
+// columns; a variant of its own, so the plain kernels keep their registers).
+template <class G, int W, int TS, int P, int MV, int XB, bool GR = false>
 __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     const int lane = threadIdx.x & 63;
@@ -1378,6 +1430,7 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
     bool scaled = false;  // wave-uniform: this wave's rows carry range factors
 
     int chunk = 0, tt = 0;
+    Greedy gr[4] = {Greedy::none(), Greedy::none(), Greedy::none(), Greedy::none()};
     auto store = [&](int tile, const f32x4 &v) {
         const int col = tile * 16 + r16;
 #pragma unroll
@@ -1385,10 +1438,15 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
             const int m = spread_out(g, i, (p.M + 3) >> 2, p.M);
             if (m >= 0) {
                 const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
-                if (p.out_type == 0)
+                if constexpr (GR) {
+                    const float c = soft_capped(v[i], p.cap);
+                    ((float *)p.out)[o] = c;
+                    if (i < MV) gr[i].add(c, col);  // rows per lane group <= MV
+                } else if (p.out_type == 0) {
                     ((float *)p.out)[o] = v[i];
-                else
+                } else {
                     ((uint16_t *)p.out)[o] = (uint16_t)f2bf(v[i]);
+                }
             }
         }
     };
@@ -1464,6 +1522,25 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
         }
     } else {
         for (int t = 0; t < nt; ++t) end_tile(f32x4{0.f, 0.f, 0.f, 0.f});
+    }
+    if constexpr (GR) {
+        // per row, over the workgroup's columns: lane groups, then waves through the partial
+        // slots of the chunk parity not read last (every wave finished reading them before
+        // the last chunk's barrier)
+        Greedy *red = (Greedy *)(part + (size_t)(chunk & 1) * TS * W * 64);  // [W][4 g][4 i]
+#pragma unroll
+        for (int i = 0; i < MV; ++i) gr[i].group16();
+        if (r16 == 0) {
+#pragma unroll
+            for (int i = 0; i < MV; ++i) red[(wave * 4 + g) * 4 + i] = gr[i];
+        }
+        lds_barrier();
+        if (wave == 0 && lane < p.M) {  // row `lane` is element i = lane % rpg of lane group lane / rpg
+            const int rpg = (p.M + 3) >> 2, g2 = lane / rpg, i2 = lane - g2 * rpg;
+            Greedy b = red[g2 * 4 + i2];
+            for (int w = 1; w < W; ++w) b.merge(red[(w * 4 + g2) * 4 + i2]);
+            b.write(p.amax_val, p.amax_idx, (size_t)lane * gridDim.x + blockIdx.x);
+        }
     }
 }
 
@@ -1629,6 +1706,9 @@ JV_QMV6(1, 4, 8)
 #define JV_QMVP(NAME, G, W, MV, XB)                                                          \
     extern "C" __global__ __launch_bounds__(64 * W) void jv_qmvp_##NAME##_m##MV(QmmParams p) { \
         qmvp_body<G, W, 2, 4, MV, XB>(p);                                                    \
+    }                                                                                         \
+    extern "C" __global__ __launch_bounds__(64 * W) void jv_qmvp_##NAME##_m##MV##_g(QmmParams p) { \
+        qmvp_body<G, W, 2, 4, MV, XB, true>(p);                                              \
     }
 // Activation loads in flight per lane (XB) cover the rows a variant stages: up to 4, 8 or 16.
 JV_QMVP(q4k, GQ4K, 8, 1, 4)
@@ -2054,7 +2134,10 @@ struct DF {  // any format with the F* interface of the small-tile kernel
 //
 // Each output element is the same MFMA chain over K as in the other tiled kernels (32-k steps
 // in order, lane group g holding k 32s + 8g .. +8), so the result is bitwise identical to theirs.
-template <class D, int TM, int TN, int WM, int WN, bool HB = false, bool APRIV = false, int NVS = 3>
+// GR: the greedy epilogue (FP32 outputs soft-capped, per-row partial argmax of the tile's
+// columns; a variant of its own).
+template <class D, int TM, int TN, int WM, int WN, bool HB = false, bool APRIV = false, int NVS = 3,
+          bool GR = false>
 __device__ __forceinline__ void gemm_body(const GemmParams &p) {
     constexpr int W = WM * WN, MT = TM / WM, NT = TN / WN;
     // activation fragments a wave loads per stage (own m slots): a share of its MT, or with
@@ -2254,6 +2337,11 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 
     // epilogue: lane (g, r) holds column r, rows 4g .. 4g + 3 of each 16 x 16 tile
     const bool f32_out = p.out_type == 0;
+    Greedy gr[MT][4];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gr[i][e] = Greedy::none();
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
 #pragma unroll
@@ -2272,13 +2360,45 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
                 if (live) {
                     const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
                     const float v = acc[i][k][e] * p.rscale[pr];  // exact: a power of two
-                    if (p.splits > 1)
+                    if constexpr (GR) {  // ungrouped, whole K, FP32 outputs (the host's rule)
+                        const float c = soft_capped(v, p.cap);
+                        ((float *)p.out)[o] = c;
+                        gr[i][e].add(c, col);
+                    } else if (p.splits > 1) {
                         p.part[(int64_t)blockIdx.z * p.split_stride + (int64_t)o] = v;
-                    else if (f32_out)
+                    } else if (f32_out) {
                         ((float *)p.out)[o] = v;
-                    else
+                    } else {
                         ((uint16_t *)p.out)[o] = (uint16_t)f2bf(v);
+                    }
                 }
+            }
+        }
+    }
+    if constexpr (GR) {
+        // per row over the tile's columns: the 16 lanes of a group, then the WN waves that
+        // share the row, through the LDS buffers (every wave is past its last stage's reads
+        // after the first barrier)
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) gr[i][e].group16();
+        lds_barrier();
+        Greedy *red = (Greedy *)smem;  // [16 TM rows][WN]
+        if (r == 0) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) red[(m_of(i) * 16 + 4 * g + e) * WN + nh] = gr[i][e];
+        }
+        lds_barrier();
+        for (int t = (int)threadIdx.x; t < 16 * TM; t += 64 * W) {
+            const int pr = mt0 * 16 + t;
+            if (pr < p.M) {
+                Greedy b = red[t * WN];
+#pragma unroll
+                for (int c = 1; c < WN; ++c) b.merge(red[t * WN + c]);
+                b.write(p.amax_val, p.amax_idx, (size_t)pr * gridDim.x + blockIdx.x);
             }
         }
     }
@@ -2438,6 +2558,14 @@ JV_GEMMP(q8_0, DF<FQ8_0>, 8, 8, 4, 2, 128, 128, r, 3)
 JV_GEMMP(q4k, DQ4K, 2, 4, 2, 2, 32, 64, r, 2)
 JV_GEMMP(q6k, DF<FQ6K>, 2, 4, 2, 2, 32, 64, r, 2)
 JV_GEMMP(q8_0, DF<FQ8_0Mix>, 2, 4, 2, 2, 32, 64, r, 2)
+// the 32 x 64 tiles with the greedy epilogue (vocabulary projections of up to 32 rows)
+#define JV_GEMMG(NAME, D)                                                                     \
+    extern "C" __global__ __launch_bounds__(256) void jv_gemm_##NAME##_32x64r_g(GemmParams p) { \
+        gemm_body<D, 2, 4, 2, 2, true, true, 2, true>(p);                                     \
+    }
+JV_GEMMG(q4k, DQ4K)
+JV_GEMMG(q6k, DF<FQ6K>)
+JV_GEMMG(q8_0, DF<FQ8_0Mix>)
 extern "C" __global__ __launch_bounds__(512) void jv_gemm_q4k_64x64r8(GemmParams p) { gemm8_body<DQ4K>(p); }
 extern "C" __global__ __launch_bounds__(512) void jv_gemm_q6k_64x64r8(GemmParams p) { gemm8_body<DF<FQ6KMix>>(p); }
 extern "C" __global__ __launch_bounds__(512) void jv_gemm_q8_0_64x64r8(GemmParams p) { gemm8_body<DF<FQ8_0Mix>>(p); }
@@ -2544,7 +2672,7 @@ extern "C" __global__ __launch_bounds__(256) void jv_repack_q5_0(RepackParams p)
 // In-place final-logit soft capping: x = cap tanh(x / cap).
 extern "C" __global__ __launch_bounds__(256) void jv_softcap(float *x, int64_t len, float cap) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < len) x[i] = cap * tanhf(x[i] / cap);
+    if (i < len) x[i] = soft_capped(x[i], cap);
 }
 
 // One workgroup per (row, token) pair: thread i covers K unit i / 4 and lane group i % 4 of the
@@ -2700,14 +2828,6 @@ extern "C" __global__ __launch_bounds__(1024) void jv_group_routes(const uint32_
             }
             if (lane == first) cnt[wv][ef] = cnt[wv][ef] + (uint32_t)__popcll(same);
         }
-    }
-}
-
-__device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
-    // (v, i) replaces (bv, bi) if larger, or equal with a lower index.
-    if (v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
     }
 }
 

@@ -31,6 +31,10 @@ struct QmmParams {
     // Tiled kernels: per input row, the factor that undoes the row's range scale (multiplied
     // into its outputs); null for none. The activations were then prescaled FP16 rows.
     const float *rscale;
+    // Greedy epilogue (persistent small-row kernels; GreedyArgs below)
+    float cap;
+    float *amax_val;
+    int32_t *amax_idx;
 };
 
 // Decode probe: rows [row0, row0 + rows) of a weight matrix into [rows][K].
@@ -82,6 +86,14 @@ struct GemmParams {
     float *part;
     int64_t split_stride;
     int32_t splits;
+    // Greedy epilogue (ungrouped, whole K, FP32 outputs): with amax_val set, every output value
+    // is first soft-capped, cap tanh(v / cap), when cap > 0, then stored, and each workgroup
+    // writes, per output row it covers, the largest of its columns' values and that value's
+    // first column to amax_val / amax_idx [M][gridDim.x] at column blockIdx.x (index -1 when
+    // one of the values is not finite). The same fields close QmmParams.
+    float cap;
+    float *amax_val;
+    int32_t *amax_idx;
 };
 
 // GGML blocks (device copy of the upload) -> device layout.

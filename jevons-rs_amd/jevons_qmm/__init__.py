@@ -90,6 +90,7 @@ def lib() -> C.CDLL:
         "jv_matmul_split": (I, [P, P, I, S, S, P, P, I, S, U32, U32, U32, P, P]),
         "jv_f16_matmul": (I, [P, P, S, S, P, S, P, P]),
         "jv_argmax_rows": (I, [P, P, S, S, P, P, P]),
+        "jv_matmul_argmax": (I, [P, P, I, S, S, P, P, S, C.c_float, P, P, P]),
         "jv_dequant_rows_f32": (I, [P, P, S, S, P, P]),
         "jv_dequant_rows_f16": (I, [P, P, S, S, P, P]),
         "jv_group_routes": (I, [P, P, S, S, U32, P, P, P, S, P]),
@@ -608,6 +609,19 @@ def argmax_rows(gpu: Gpu, logits, scratch: SplitScratch, stream=None):
     idx = torch.empty(rows, dtype=torch.int32, device=logits.device)
     _check(lib().jv_argmax_rows(gpu.handle, _dev(logits), rows, n, _dev(idx), scratch.handle,
                                 _stream(stream)))
+    return idx
+
+
+def matmul_argmax(gpu: Gpu, x, m: int, w: QMatrix, out, cap: float, scratch: SplitScratch, stream=None):
+    """The vocabulary projection's logits into float32 `out` [m, n], soft-capped when cap > 0,
+    and greedy's argmax of every row (crates/jevons-gemma4-diffusion/src/model.rs:1192-1204, then
+    crates/jevons-core/src/model.rs:207-219 per row): the int32 indices, -1 for a row holding a
+    non-finite value."""
+    import torch
+
+    idx = torch.empty(m, dtype=torch.int32, device=out.device)
+    _check(lib().jv_matmul_argmax(gpu.handle, _dev(x), _act(x), x.numel(), m, w.handle, _dev(out),
+                                  out.numel(), cap, _dev(idx), scratch.handle, _stream(stream)))
     return idx
 
 

@@ -1,0 +1,116 @@
+"""GPU: the vocabulary projection with its soft cap and greedy's argmax in one call
+(jv_matmul_argmax; crates/jevons-gemma4-diffusion/src/model.rs:1192-1204, then greedy per row,
+crates/jevons-core/src/model.rs:207-219).
+
+Bars: the logits and indices equal, bit for bit, those of jv_matmul, jv_softcap_logits and
+jv_argmax_rows in turn, on every kernel family the call takes (persistent small-row kernels and
+32 x 64 tiles with the fused epilogue, the other plans through the three steps); every index is
+greedy's (the oracle's restatement of model.rs:207-219) on the same logits: first maximum on
+ties, -1 for a row holding a non-finite value.
+"""
+import numpy as np
+import pytest
+import torch
+
+import jevons_qmm as jq
+import oracle as O
+from helpers import activations, say
+from jevons_qmm import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    yield jq.Gpu(0)
+
+
+def _greedy_or_invalid(row):
+    try:
+        return O.greedy(row)[0]
+    except O.OracleError:
+        return -1
+
+
+def _three_steps(gpu, x, m, w, n, cap, scratch):
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    jq.matmul(gpu, x, m, w, out, scratch)
+    if cap > 0:
+        jq.softcap_logits(gpu, out, cap)
+    return out, jq.argmax_rows(gpu, out, scratch)
+
+
+def _fused(gpu, x, m, w, n, cap, scratch):
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    idx = jq.matmul_argmax(gpu, x, m, w, out, cap, scratch)
+    return out, idx
+
+
+KINDS = [jq.Q4K, jq.Q6K, jq.Q8_0]
+
+
+@pytest.mark.parametrize("kind", KINDS, ids=["q4k", "q6k", "q8_0"])
+@pytest.mark.parametrize("m", [1, 3, 8, 20, 32, 48])
+@pytest.mark.parametrize("cap", [0.0, 30.0])
+def test_matmul_argmax_equals_the_three_steps(gpu, kind, m, cap):
+    """N = 32768 (wide enough for the persistent kernels at M <= 2), K = 512. The weight row j*
+    that holds row 0's largest logit is copied into every row j* mod 2048 + 2048 t (other
+    workgroups, the same lane and tile position, so the copies' logits are equal bit for bit),
+    so greedy must take the first copy, j* mod 2048; row 1 is all zeros (every logit ties:
+    index 0) and, from M = 3, row 2 holds a NaN (-1)."""
+    n, k = 32768, 512
+    raw = synth.weights(kind, 9, n, k).copy()
+    x32 = synth.normal_rows(5, m, k)
+    if m >= 2:
+        x32[1] = 0.0
+    if m >= 3:
+        x32[2, 5] = np.nan
+    x, _ = activations("bf16", x32)
+    scratch = jq.SplitScratch(gpu)
+    first, _ = _three_steps(gpu, x, m, jq.QMatrix.upload(gpu, kind, n, k, 1, raw), n, 0.0, scratch)
+    jstar = O.greedy(first[0].cpu().numpy())[0]
+    rows = raw.reshape(n, raw.size // n)
+    for t in range(n // 2048):
+        rows[jstar % 2048 + 2048 * t] = rows[jstar]
+    w = jq.QMatrix.upload(gpu, kind, n, k, 1, raw)
+    ref_out, ref_idx = _three_steps(gpu, x, m, w, n, cap, scratch)
+    out, idx = _fused(gpu, x, m, w, n, cap, scratch)
+    assert torch.equal(out.isnan(), ref_out.isnan())
+    assert torch.equal(torch.nan_to_num(out), torch.nan_to_num(ref_out))
+    assert torch.equal(idx, ref_idx)
+    host, got = out.cpu().numpy(), idx.cpu().numpy()
+    for r in range(m):
+        assert got[r] == _greedy_or_invalid(host[r]), r
+    if cap == 0:  # soft-capped logits may saturate into ties at lower columns
+        assert got[0] == jstar % 2048, (jstar, got[0])
+    if m >= 2:
+        assert got[1] == 0
+    if m >= 3:
+        assert got[2] == -1
+    say("kind", kind, "m", m, "cap", cap, "j*", jstar, "indices", got[:8])
+
+
+def test_matmul_argmax_on_repeated_calls_and_other_inputs(gpu):
+    """Two products in a row on one scratch, the second smaller and on other weights: each
+    call's indices are its own greedy (no stale partials)."""
+    scratch = jq.SplitScratch(gpu)
+    for seed, m, n, k in ((3, 8, 65536, 1024), (4, 2, 32768, 512)):
+        raw = synth.weights(jq.Q6K, seed, n, k)
+        w = jq.QMatrix.upload(gpu, jq.Q6K, n, k, 1, raw)
+        x, _ = activations("bf16", synth.normal_rows(seed, m, k))
+        out, idx = _fused(gpu, x, m, w, n, 30.0, scratch)
+        ref_out, ref_idx = _three_steps(gpu, x, m, w, n, 30.0, scratch)
+        assert torch.equal(out, ref_out) and torch.equal(idx, ref_idx)
+        host = out.cpu().numpy()
+        assert [int(i) for i in idx.cpu()] == [O.greedy(host[r])[0] for r in range(m)]
+
+
+def test_matmul_argmax_rejects_bad_arguments(gpu):
+    n, k = 32768, 256
+    w = jq.QMatrix.upload(gpu, jq.Q4K, n, k, 1, synth.weights(jq.Q4K, 1, n, k))
+    x, _ = activations("bf16", synth.normal_rows(1, 1, k))
+    out = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    scratch = jq.SplitScratch(gpu)
+    for cap in (-1.0, float("inf"), float("nan")):
+        with pytest.raises(jq.JvError, match="softcap"):
+            jq.matmul_argmax(gpu, x, 1, w, out, cap, scratch)

@@ -9,7 +9,8 @@ f64 matmul):
 - the Q6_K vocabulary projection over the whole vocabulary (K = 3840, N = 262144) at M = 1, 8
   (persistent small-row kernels) and 32 (32 x 64 tiles), with the per-row argmax of the raw and
   of the soft-capped logits (greedy, crates/jevons-core/src/model.rs:207-219; softcap,
-  crates/jevons-gemma4-diffusion/src/gpu/ops.rs:750-758);
+  crates/jevons-gemma4-diffusion/src/gpu/ops.rs:750-758), and the same through the fused call
+  (jv_matmul_argmax) bit for bit;
 - the Q8_0 GEMV at K = N = 4096 with f32 activations.
 
 Bars: outputs within 1e-3 of max|f64 oracle|; whole-K plans bitwise identical to each other;
@@ -175,11 +176,23 @@ def test_q6k_lm_head_full_vocabulary(gpu, vocab, m):
     bound = 2 * float(np.max(np.abs(got[rows] - want)))
     close = _argmax_checks(gpu, out, wmap, bound, "logits")
     cap = 30.0
+    _fused_equals(gpu, x, m, w, n, out, 0.0)
     jq.softcap_logits(gpu, out, cap)
     smap = {r: O.softcap(v, cap) for r, v in wmap.items()}
     # tanh is 1-Lipschitz after scaling, and the device tanh adds at most a few ulp of cap
     close_sc = _argmax_checks(gpu, out, smap, bound + 8e-6 * cap, "softcapped")
+    _fused_equals(gpu, x, m, w, n, out, cap)
     say("rows within the error bound of a tie:", close, "raw,", close_sc, "soft-capped, of", len(rows))
+
+
+def _fused_equals(gpu, x, m, w, n, logits, cap):
+    """jv_matmul_argmax (product, soft cap and argmax fused) gives `logits` (already soft-capped
+    when cap > 0) and their argmax_rows indices bit for bit."""
+    scratch = jq.SplitScratch(gpu)
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    idx = jq.matmul_argmax(gpu, x, m, w, out, cap, scratch)
+    assert torch.equal(out, logits), cap
+    assert torch.equal(idx, jq.argmax_rows(gpu, logits, scratch)), cap
 
 
 @pytest.mark.parametrize("m", [1, 4])
