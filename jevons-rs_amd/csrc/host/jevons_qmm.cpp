@@ -600,9 +600,11 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     if (grp && plan.splits > 1) return fail(JV_ERR_INVALID, "grouped pipelined tiles do not split K");
     const int jobs_or_tiles = grp ? (int)grp->max_jobs : (int)((m + plan.bm - 1) / plan.bm);
     const int mtiles = jobs_or_tiles * (int)(plan.bm / 16);
-    // the greedy epilogue exists on the 32 x 64 register tiles (ungrouped, whole K, FP32 out)
-    const bool greedy = gr && !grp && plan.splits == 1 && plan.bm == 32 && plan.bn == 64 &&
-                        reg_format(w) && out_type == JV_OUT_F32;
+    // the greedy epilogue exists on the register tiles of Q4_K, Q6_K and Q8_0 (ungrouped, whole
+    // K, FP32 out; 64 x 64 on its 8-wave tile)
+    const char *regenv = getenv("JV_GEMM_REG");
+    const bool reg = reg_format(w) && (plan.bm == 32 || !(regenv && regenv[0] == '0'));
+    const bool greedy = gr && !grp && plan.splits == 1 && reg && out_type == JV_OUT_F32;
     const int slots = (int)(w->n / plan.bn);
     // fragments, then each packed row's range factor
     const size_t frag_bytes = (size_t)mtiles * 16 * w->k * 2;
@@ -648,9 +650,7 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     char name[40];
     // Q4_K, Q6_K and Q8_0 tiles run on waves that keep their activation fragments in
     // registers (same bits as the tiles that share them through LDS; JV_GEMM_REG=0 selects
-    // those, except for 32 x 64, which exists only with register fragments).
-    const char *regenv = getenv("JV_GEMM_REG");
-    const bool reg = reg_format(w) && (plan.bm == 32 || !(regenv && regenv[0] == '0'));
+    // those, except for 32 x 64, which exists only with register fragments): `reg` above.
     // Ungrouped 64 x 64 products run the 8-wave tile (two waves per SIMD); expert jobs keep the
     // 4-wave one, faster there.
     const bool w8 = reg && !grp && plan.bm == 64;

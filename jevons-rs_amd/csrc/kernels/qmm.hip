@@ -2415,7 +2415,8 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
 // down projection 89 against 97 us, q/k/v/o 10-14 % faster. Ungrouped products only: expert
 // jobs (thousands of workgroups, already several per CU) ran slower on it (169 against 149 us
 // on 128 experts x 32 rows).
-template <class D>
+// GR: the greedy epilogue, as in gemm_body.
+template <class D, bool GR = false>
 __device__ __forceinline__ void gemm8_body(const GemmParams &p) {
     constexpr int UPS = 8 / D::SPU;
     constexpr int LEAD = 3;
@@ -2499,6 +2500,7 @@ __device__ __forceinline__ void gemm8_body(const GemmParams &p) {
     for (int j = 0; j < 8; ++j) step(8 * (U8 - 1) + j, j, true);
 
     const bool f32_out = p.out_type == 0;
+    Greedy gr[4] = {Greedy::none(), Greedy::none(), Greedy::none(), Greedy::none()};
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int col = (t0 + 2 * nh + k) * 16 + r;
@@ -2508,13 +2510,37 @@ __device__ __forceinline__ void gemm8_body(const GemmParams &p) {
             if (m < p.M) {
                 const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
                 const float v = acc[k][e] * p.rscale[m];  // exact: a power of two
-                if (p.splits > 1)
+                if constexpr (GR) {  // ungrouped, whole K, FP32 outputs (the host's rule)
+                    const float c = soft_capped(v, p.cap);
+                    ((float *)p.out)[o] = c;
+                    gr[e].add(c, col);
+                } else if (p.splits > 1) {
                     p.part[(int64_t)blockIdx.z * p.split_stride + (int64_t)o] = v;
-                else if (f32_out)
+                } else if (f32_out) {
                     ((float *)p.out)[o] = v;
-                else
+                } else {
                     ((uint16_t *)p.out)[o] = (uint16_t)f2bf(v);
+                }
             }
+        }
+    }
+    if constexpr (GR) {
+        // per row over the tile's 64 columns: the 16 lanes of a group, then the two waves
+        // (nh = 0, 1) of the m-tile through the stage buffers, after a barrier
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gr[e].group16();
+        lds_barrier();
+        Greedy *red = (Greedy *)smem;  // [64 rows][2]
+        if (r == 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) red[(mq * 16 + 4 * g + e) * 2 + nh] = gr[e];
+        }
+        lds_barrier();
+        const int t = (int)threadIdx.x, pr = mt0 * 16 + t;
+        if (t < 64 && pr < p.M) {
+            Greedy b = red[2 * t];
+            b.merge(red[2 * t + 1]);
+            b.write(p.amax_val, p.amax_idx, (size_t)pr * gridDim.x + blockIdx.x);
         }
     }
 }
@@ -2558,15 +2584,25 @@ JV_GEMMP(q8_0, DF<FQ8_0>, 8, 8, 4, 2, 128, 128, r, 3)
 JV_GEMMP(q4k, DQ4K, 2, 4, 2, 2, 32, 64, r, 2)
 JV_GEMMP(q6k, DF<FQ6K>, 2, 4, 2, 2, 32, 64, r, 2)
 JV_GEMMP(q8_0, DF<FQ8_0Mix>, 2, 4, 2, 2, 32, 64, r, 2)
-// the 32 x 64 tiles with the greedy epilogue (vocabulary projections of up to 32 rows)
-#define JV_GEMMG(NAME, D)                                                                     \
-    extern "C" __global__ __launch_bounds__(256) void jv_gemm_##NAME##_32x64r_g(GemmParams p) { \
-        gemm_body<D, 2, 4, 2, 2, true, true, 2, true>(p);                                     \
+// The register tiles above with the greedy epilogue (vocabulary projections): the same
+// template arguments and a _g suffix.
+#define JV_GEMMG(NAME, D, TM, TN, WM, WN, ROWS, COLS, HB, APRIV, NV)                          \
+    extern "C" __global__ __launch_bounds__(64 * WM * WN) void jv_gemm_##NAME##_##ROWS##x##COLS##r_g(GemmParams p) { \
+        gemm_body<D, TM, TN, WM, WN, HB, APRIV, NV, true>(p);                                 \
     }
-JV_GEMMG(q4k, DQ4K)
-JV_GEMMG(q6k, DF<FQ6K>)
-JV_GEMMG(q8_0, DF<FQ8_0Mix>)
+JV_GEMMG(q4k, DQ4K, 2, 4, 2, 2, 32, 64, true, true, 2)
+JV_GEMMG(q6k, DF<FQ6K>, 2, 4, 2, 2, 32, 64, true, true, 2)
+JV_GEMMG(q8_0, DF<FQ8_0Mix>, 2, 4, 2, 2, 32, 64, true, true, 2)
+JV_GEMMG(q4k, DQ4K, 8, 8, 4, 2, 128, 128, true, true, 1)
+JV_GEMMG(q6k, DF<FQ6K>, 8, 8, 4, 2, 128, 128, true, true, 1)
+JV_GEMMG(q8_0, DF<FQ8_0>, 8, 8, 4, 2, 128, 128, true, true, 3)
+JV_GEMMG(q4k, DQ4K, 16, 8, 8, 1, 256, 128, true, false, 4)
+JV_GEMMG(q6k, DF<FQ6K>, 16, 8, 8, 1, 256, 128, true, false, 5)
+JV_GEMMG(q8_0, DF<FQ8_0>, 16, 8, 4, 2, 256, 128, true, true, 3)
 extern "C" __global__ __launch_bounds__(512) void jv_gemm_q4k_64x64r8(GemmParams p) { gemm8_body<DQ4K>(p); }
+extern "C" __global__ __launch_bounds__(512) void jv_gemm_q4k_64x64r8_g(GemmParams p) { gemm8_body<DQ4K, true>(p); }
+extern "C" __global__ __launch_bounds__(512) void jv_gemm_q6k_64x64r8_g(GemmParams p) { gemm8_body<DF<FQ6KMix>, true>(p); }
+extern "C" __global__ __launch_bounds__(512) void jv_gemm_q8_0_64x64r8_g(GemmParams p) { gemm8_body<DF<FQ8_0Mix>, true>(p); }
 extern "C" __global__ __launch_bounds__(512) void jv_gemm_q6k_64x64r8(GemmParams p) { gemm8_body<DF<FQ6KMix>>(p); }
 extern "C" __global__ __launch_bounds__(512) void jv_gemm_q8_0_64x64r8(GemmParams p) { gemm8_body<DF<FQ8_0Mix>>(p); }
 JV_GEMM_TILES(q4k, DQ4K)

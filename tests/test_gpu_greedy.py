@@ -50,10 +50,12 @@ KINDS = [jq.Q4K, jq.Q6K, jq.Q8_0]
 
 
 @pytest.mark.parametrize("kind", KINDS, ids=["q4k", "q6k", "q8_0"])
-@pytest.mark.parametrize("m", [1, 3, 8, 20, 32, 48])
+@pytest.mark.parametrize("m", [1, 3, 8, 20, 32, 48, 128, 200])
 @pytest.mark.parametrize("cap", [0.0, 30.0])
 def test_matmul_argmax_equals_the_three_steps(gpu, kind, m, cap):
-    """N = 32768 (wide enough for the persistent kernels at M <= 2), K = 512. The weight row j*
+    """N = 32768 (wide enough for the persistent kernels at M <= 2), K = 512: persistent
+    small-row kernels up to M = 16, then the 32 x 64, 64 x 64 (8-wave), 128 x 128 and 256 x 128
+    register tiles (M = 200: 56 rows of padding). The weight row j*
     that holds row 0's largest logit is copied into every row j* mod 2048 + 2048 t (other
     workgroups, the same lane and tile position, so the copies' logits are equal bit for bit),
     so greedy must take the first copy, j* mod 2048; row 1 is all zeros (every logit ties:
@@ -91,10 +93,11 @@ def test_matmul_argmax_equals_the_three_steps(gpu, kind, m, cap):
 
 
 def test_matmul_argmax_on_repeated_calls_and_other_inputs(gpu):
-    """Two products in a row on one scratch, the second smaller and on other weights: each
+    """Products in a row on one scratch, each smaller and on other weights, the last on the
+    per-tile small-row kernel (M = 1 of a narrow matrix), which runs the three steps: each
     call's indices are its own greedy (no stale partials)."""
     scratch = jq.SplitScratch(gpu)
-    for seed, m, n, k in ((3, 8, 65536, 1024), (4, 2, 32768, 512)):
+    for seed, m, n, k in ((3, 8, 65536, 1024), (4, 2, 32768, 512), (5, 1, 4096, 512)):
         raw = synth.weights(jq.Q6K, seed, n, k)
         w = jq.QMatrix.upload(gpu, jq.Q6K, n, k, 1, raw)
         x, _ = activations("bf16", synth.normal_rows(seed, m, k))
