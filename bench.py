@@ -356,17 +356,24 @@ def measure_configs(gpu, steps):
         out = torch.empty((m, n), dtype=torch.float32, device="cuda")
         jq.matmul(gpu, x, m, ms[0], out, scratch)
         jq.argmax_rows(gpu, out, scratch)
-        t = kernel_time_ms(lambda r: jq.matmul(gpu, x, m, ms[0], out, scratch), max(4, steps // 10))
-        ta = kernel_time_ms(lambda r: jq.argmax_rows(gpu, out, scratch), max(4, steps // 10))
-
         def three_steps(r):  # the reference's order: product, soft cap, greedy per row
             jq.matmul(gpu, x, m, ms[0], out, scratch)
             jq.softcap_logits(gpu, out, 30.0)
             jq.argmax_rows(gpu, out, scratch)
 
-        t3 = kernel_time_ms(three_steps, max(4, steps // 10))
-        tf = kernel_time_ms(lambda r: jq.matmul_argmax(gpu, x, m, ms[0], out, 30.0, scratch), max(4, steps // 10))
-        tf0 = kernel_time_ms(lambda r: jq.matmul_argmax(gpu, x, m, ms[0], out, 0.0, scratch), max(4, steps // 10))
+        # the product alone, the argmax alone, the three steps, and the product with the soft
+        # cap and greedy fused (cap 30, and cap 0: greedy only); five interleaved rounds,
+        # medians, so that the differences are not the drift between separate timings
+        fns = [lambda r: jq.matmul(gpu, x, m, ms[0], out, scratch),
+               lambda r: jq.argmax_rows(gpu, out, scratch),
+               three_steps,
+               lambda r: jq.matmul_argmax(gpu, x, m, ms[0], out, 30.0, scratch),
+               lambda r: jq.matmul_argmax(gpu, x, m, ms[0], out, 0.0, scratch)]
+        runs = [[] for _ in fns]
+        for _ in range(5):
+            for fn, rr in zip(fns, runs):
+                rr.append(kernel_time_ms(fn, max(4, steps // 10)))
+        t, ta, t3, tf, tf0 = (statistics.median(rr) for rr in runs)
         gbs = wbytes / (t * 1e-3) / 1e9
         lm[str(m)] = {"kernel_us": round(t * 1e3, 2), "weight_GBps": round(gbs, 1),
                       "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),

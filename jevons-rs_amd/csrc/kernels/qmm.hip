@@ -2949,19 +2949,35 @@ extern "C" __global__ __launch_bounds__(256) void jv_argmax_partial(const float 
 }
 
 // Grid (rows), 256 threads: combine the partials of each row; -1 if any range was non-finite or
-// the row is empty.
+// the row is empty. Each thread issues the loads of eight partials before it compares them (a
+// row's thousands of partials in one or two round trips). Partials past the row's end read as
+// (-inf, INT_MAX), which never replaces a result: valid partials are finite.
 extern "C" __global__ __launch_bounds__(256) void jv_argmax_final(const float *pval, const int *pidx,
                                                                   int chunks, int *index) {
     const int row = blockIdx.x;
+    const float *pv = pval + (int64_t)row * chunks;
+    const int *pi = pidx + (int64_t)row * chunks;
     float bv = -__builtin_inff();
     int bi = 0x7fffffff;
     int bad = 0;
-    for (int c = threadIdx.x; c < chunks; c += 256) {
-        const int i = pidx[(int64_t)row * chunks + c];
-        if (i < 0)
-            bad = 1;
-        else
-            better(bv, bi, pval[(int64_t)row * chunks + c], i);
+    constexpr int kBatch = 8;
+    for (int c0 = 0; c0 < chunks; c0 += 256 * kBatch) {
+        float v[kBatch];
+        int i[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int c = c0 + j * 256 + (int)threadIdx.x;
+            const bool in = c < chunks;
+            v[j] = in ? pv[c] : -__builtin_inff();
+            i[j] = in ? pi[c] : 0x7fffffff;
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            if (i[j] < 0)
+                bad = 1;
+            else
+                better(bv, bi, v[j], i[j]);
+        }
     }
     group_best(bv, bi, bad);
     if (threadIdx.x == 0) index[row] = (bad || chunks == 0) ? -1 : bi;
