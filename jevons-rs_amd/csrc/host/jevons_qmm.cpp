@@ -396,6 +396,15 @@ struct GreedyArgs {
     bool fused = false;
 };
 
+// jv_argmax_final over `rows` rows of `chunks` partials: one workgroup per row, of enough waves
+// (4 to 16) that each thread loads at most eight partials at once where possible.
+jv_status launch_argmax_final(jv_ctx *ctx, float *pval, int32_t *pidx, int chunks, size_t rows,
+                              int32_t *index, void *stream) {
+    const unsigned threads = (unsigned)std::min(1024, std::max(256, (chunks + 7) / 8 + 63) / 64 * 64);
+    void *a2[] = {&pval, &pidx, &chunks, &index};
+    return launch(ctx, "jv_argmax_final", dim3((unsigned)rows), dim3(threads), 0, stream, a2);
+}
+
 // Records the partials of `rows` x `slots` workgroup columns at `payload` (values, then indices).
 void greedy_partials(GreedyArgs *gr, size_t rows, int slots, void *payload) {
     gr->val = (float *)payload;
@@ -1403,8 +1412,7 @@ jv_status jv_argmax_rows(jv_ctx *ctx, const float *logits, size_t rows, size_t n
                     stream, a1);
         if (st != JV_OK) return st;
     }
-    void *a2[] = {&pval, &pidx, &chunks, &index};
-    return launch(ctx, "jv_argmax_final", dim3((unsigned)rows), dim3(256), 0, stream, a2);
+    return launch_argmax_final(ctx, pval, pidx, chunks, rows, index, stream);
 }
 
 jv_status jv_matmul_argmax(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
@@ -1427,11 +1435,7 @@ jv_status jv_matmul_argmax(jv_ctx *ctx, const void *x, jv_act act, size_t x_len,
     jv_status st = run_product(ctx, x, act, x_len, m, w, out, JV_OUT_F32, out_len, plan, scratch, stream, &gr);
     if (st != JV_OK || m == 0) return st;
     if (gr.fused) {
-        float *pval = gr.val;
-        int32_t *pidx = gr.idx;
-        int chunks = gr.slots;
-        void *a2[] = {&pval, &pidx, &chunks, &index};
-        return launch(ctx, "jv_argmax_final", dim3((unsigned)m), dim3(256), 0, stream, a2);
+        return launch_argmax_final(ctx, gr.val, gr.idx, gr.slots, m, index, stream);
     }
     if (cap > 0.f) {
         st = jv_softcap_logits(ctx, out, m * w->n, cap, stream);

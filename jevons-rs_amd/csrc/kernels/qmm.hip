@@ -2877,10 +2877,11 @@ __device__ __forceinline__ void wave_best(float &v, int &i) {
     }
 }
 
-// (max, index) of a 256-thread workgroup; thread 0 holds the result. `bad` is or-ed the same way.
+// (max, index) of a workgroup of up to 16 waves; thread 0 holds the result. `bad` is or-ed the
+// same way.
 __device__ __forceinline__ void group_best(float &v, int &i, int &bad) {
-    __shared__ float sv[4];
-    __shared__ int si[4], sb[4];
+    __shared__ float sv[16];
+    __shared__ int si[16], sb[16];
     wave_best(v, i);
     bad = __any(bad) ? 1 : 0;
     const int wave = threadIdx.x >> 6;
@@ -2891,7 +2892,7 @@ __device__ __forceinline__ void group_best(float &v, int &i, int &bad) {
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) {
             better(v, i, sv[w], si[w]);
             bad |= sb[w];
         }
@@ -2948,12 +2949,12 @@ extern "C" __global__ __launch_bounds__(256) void jv_argmax_partial(const float 
     }
 }
 
-// Grid (rows), 256 threads: combine the partials of each row; -1 if any range was non-finite or
-// the row is empty. Each thread issues the loads of eight partials before it compares them (a
-// row's thousands of partials in one or two round trips). Partials past the row's end read as
-// (-inf, INT_MAX), which never replaces a result: valid partials are finite.
-extern "C" __global__ __launch_bounds__(256) void jv_argmax_final(const float *pval, const int *pidx,
-                                                                  int chunks, int *index) {
+// Grid (rows), 256 to 1024 threads (a multiple of 64): combine the partials of each row; -1 if
+// any range was non-finite or the row is empty. Each thread issues the loads of eight partials
+// before it compares them (a row's thousands of partials in one round trip). Partials past the
+// row's end read as (-inf, INT_MAX), which never replaces a result: valid partials are finite.
+extern "C" __global__ __launch_bounds__(1024) void jv_argmax_final(const float *pval, const int *pidx,
+                                                                   int chunks, int *index) {
     const int row = blockIdx.x;
     const float *pv = pval + (int64_t)row * chunks;
     const int *pi = pidx + (int64_t)row * chunks;
@@ -2961,12 +2962,13 @@ extern "C" __global__ __launch_bounds__(256) void jv_argmax_final(const float *p
     int bi = 0x7fffffff;
     int bad = 0;
     constexpr int kBatch = 8;
-    for (int c0 = 0; c0 < chunks; c0 += 256 * kBatch) {
+    const int nt = (int)blockDim.x;
+    for (int c0 = 0; c0 < chunks; c0 += nt * kBatch) {
         float v[kBatch];
         int i[kBatch];
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
-            const int c = c0 + j * 256 + (int)threadIdx.x;
+            const int c = c0 + j * nt + (int)threadIdx.x;
             const bool in = c < chunks;
             v[j] = in ? pv[c] : -__builtin_inff();
             i[j] = in ? pi[c] : 0x7fffffff;
