@@ -1641,9 +1641,13 @@ __device__ __forceinline__ void qmvs_body(const QmmParams &p) {
     const int col = tile * 16 + (ln & 15);
     const size_t plane = (size_t)p.M * (size_t)p.N;
     if (scaled) unscale_rows(acc, Sc, lg, p.M);
-    // Partials are written and read at device scope (sc1: through to the level every compute
-    // unit sees, no cache-wide write-back or invalidate); the store acknowledgements are awaited
-    // before the count, and the reads are issued only after the count completes.
+    // Partials are written and read as agent-scope atomics (sc1: through to the level every
+    // compute unit sees, no cache-wide write-back or invalidate); the store acknowledgements are
+    // awaited before the count, and the reads are issued only after the count completes. The
+    // orderings are kept by the waits (hardware) and by asm memory clobbers (compiler), not by
+    // release / acquire: an agent-scope fence on every wave (buffer_wbl2 sc1 + buffer_inv sc1, the
+    // write-back and invalidation of the whole L2) made these kernels 4-17 times slower (Q4_K
+    // 3840 x 15360 at M = 1: 190 against 11.4 us).
     const int rpg = (p.M + 3) >> 2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1658,6 +1662,7 @@ __device__ __forceinline__ void qmvs_body(const QmmParams &p) {
         old = __hip_atomic_fetch_add(p.counters + tile, 16u / W, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = __builtin_amdgcn_readfirstlane(old);
     if (((old + 16u / W) & 15u) != 0) return;
+    asm volatile("" ::: "memory");  // no partial read is moved above the count
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = spread_out(lg, i, rpg, p.M);
