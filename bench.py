@@ -392,7 +392,7 @@ def measure_configs(gpu, steps):
                           "weight_bytes": wbytes, "per_m": lm}
     log("q6k lm_head:", res["q6k_lm_head"])
     # expert-grouped product (MoE gate/up): 128 Q4_K experts [1408, 2816], 512 tokens routed to
-    # 8 experts each (seeded uniform routing), grouped into 64-row jobs on the device
+    # 8 experts each (seeded uniform routing), grouped into jobs on the device
     experts, n, k, tokens, top_k = 128, 1408, 2816, 512, 8
     raw = synth.weights(jq.Q4K, 6, experts * n, k)
     w = jq.QMatrix.upload_device(gpu, jq.Q4K, n, k, experts, torch.from_numpy(raw).cuda())
@@ -401,13 +401,31 @@ def measure_configs(gpu, steps):
     ids = torch.from_numpy(route.astype(np.int32)).cuda()
     x = xrows(tokens, k, 8)
     out = torch.empty((tokens * top_k, n), dtype=torch.float32, device="cuda")
-    g = jq.group_routes(gpu, ids, experts, 64, in_div=top_k)
-    jq.matmul_grouped(gpu, x, w, g, out, 64, 64, 1, scratch)
-    t = kernel_time_ms(lambda r: jq.matmul_grouped(gpu, x, w, g, out, 64, 64, 1, scratch), max(4, steps // 10))
+    # the job plan as the reference picks it (Tuner::grouped, tune.rs:177-189, model.rs:803-805):
+    # the tuner's measured pick among rows {32, 64} x columns {64, 128} on its balanced routing;
+    # every candidate is also timed on this routing
+    a = tokens * top_k
+    route_cap = a
+    jobs_len = 1 + 2 * ((a + 31) // 32 + experts)
+    tbuf = {nm: torch.empty(sz, dtype=torch.int32, device="cuda")
+            for nm, sz in (("ids", route_cap), ("sorted", route_cap), ("offsets", experts + 1), ("jobs", jobs_len))}
+    tuner = jq.Tuner.new(gpu, None)
+    xt = xrows(a, k, 10)  # the tuner's input: one row per assignment (tune.rs:191-193)
+    tuner.tune_grouped([w], tokens, top_k, xt, out, tbuf["ids"], tbuf["sorted"], tbuf["offsets"], tbuf["jobs"], scratch)
+    del xt
+    pick = tuner.grouped(w, tokens)
     flops = 2.0 * tokens * top_k * n * k
+    cands = {}
+    for bm, bn in ((32, 64), (32, 128), (64, 64), (64, 128)):
+        g = jq.group_routes(gpu, ids, experts, bm, in_div=top_k)
+        jq.matmul_grouped(gpu, x, w, g, out, bm, bn, 1, scratch)
+        tc = kernel_time_ms(lambda r: jq.matmul_grouped(gpu, x, w, g, out, bm, bn, 1, scratch), max(4, steps // 10))
+        cands[f"{bm}x{bn}"] = round(tc * 1e3, 2)
+    t = cands[f"{pick[0]}x{pick[1]}"] * 1e-3
     tf = flops / (t * 1e-3) / 1e12
     res["moe_grouped"] = {"workload": f"Q4_K expert-grouped product, {experts} experts N={n} K={k}, {tokens} tokens x top-{top_k}, "
-                                      "64-row jobs, bf16 activations, f32 out",
+                                      "jobs on the tuner's plan, bf16 activations, f32 out",
+                          "plan": {"bm": pick[0], "bn": pick[1]}, "kernel_us_by_plan": cands,
                           "kernel_us": round(t * 1e3, 2), "weight_bytes": raw.size,
                           "weight_GBps": round(raw.size / (t * 1e-3) / 1e9, 1),
                           "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_F16_PEAK_TFLOPS,
