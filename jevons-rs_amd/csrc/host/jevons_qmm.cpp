@@ -176,6 +176,9 @@ namespace {
 // allocated, a multiple of 16 after every launch); partial buffers of all uses follow them.
 constexpr size_t kCounterTiles = 65536;
 constexpr size_t kCounterBytes = kCounterTiles * 4;
+// The last counter is the greedy epilogue's arrival count (zero between launches); the split-K
+// small-row kernels take at most kCounterTiles - 1 tiles.
+constexpr size_t kGreedyCounter = kCounterTiles - 1;
 
 // Size of a grown buffer: at least twice the old one, so that the buffers a context retires
 // over its life add up to less than its largest one.
@@ -390,10 +393,12 @@ struct GroupArgs {
 struct GreedyArgs {
     float cap = 0.f;
     jv_scratch *scratch = nullptr;
+    int32_t *index = nullptr;  // the rows' indices (written by the product when `done`)
     float *val = nullptr;
     int32_t *idx = nullptr;
     int slots = 0;
     bool fused = false;
+    bool done = false;  // the product's last workgroup combined the partials itself
 };
 
 // jv_argmax_final over `rows` rows of `chunks` partials: one workgroup per row, of enough waves
@@ -745,7 +750,7 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         // split-K uses the context's own, so that its rows keep the bits of every other m.
         if (!scratch && lds_tile > lmax && !(wide && lds_persist <= lmax) && stage + 64 <= lmax)
             scratch = own_scratch(ctx);
-        const bool split_ok = scratch && U >= waves && (size_t)T <= kCounterTiles && stage + 64 <= lmax;
+        const bool split_ok = scratch && U >= waves && (size_t)T <= kGreedyCounter && stage + 64 <= lmax;
         // Persistent workgroups stage the activations once for several tiles: they serve wide
         // matrices and, above 2 rows, any matrix (at m = 4-8 on the decode shapes 10-34% faster
         // than the per-tile kernels, whose staging per tile or tile pair dominates there).
@@ -801,6 +806,10 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
                     p.cap = gr->cap;
                     p.amax_val = gr->val;
                     p.amax_idx = gr->idx;
+                    // the product's last workgroup writes the indices (no jv_argmax_final)
+                    p.amax_out = gr->index;
+                    p.amax_count = (uint32_t *)gr->scratch->buf + kGreedyCounter;
+                    gr->done = true;
                 }
                 return launch(ctx, name, dim3((unsigned)grid), dim3(64 * waves), lds, stream, args);
             }
@@ -1432,8 +1441,9 @@ jv_status jv_matmul_argmax(jv_ctx *ctx, const void *x, jv_act act, size_t x_len,
     GreedyArgs gr;
     gr.cap = cap;
     gr.scratch = scratch;
+    gr.index = index;
     jv_status st = run_product(ctx, x, act, x_len, m, w, out, JV_OUT_F32, out_len, plan, scratch, stream, &gr);
-    if (st != JV_OK || m == 0) return st;
+    if (st != JV_OK || m == 0 || gr.done) return st;
     if (gr.fused) {
         return launch_argmax_final(ctx, gr.val, gr.idx, gr.slots, m, index, stream);
     }

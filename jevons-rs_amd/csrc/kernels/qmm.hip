@@ -953,7 +953,76 @@ struct Greedy {
         val[o] = v;
         idx[o] = bad ? -1 : i;
     }
+    // the same as agent-scope atomic stores, for a reader in the same launch
+    __device__ void write_shared(float *val, int32_t *idx, size_t o) const {
+        __hip_atomic_store(val + o, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(idx + o, bad ? -1 : i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // over the 64 lanes of a wave
+    __device__ void wave64() {
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float ov = __shfl_xor(v, off);
+            const int oi = __shfl_xor(i, off);
+            const int ob = __shfl_xor(bad, off);
+            better(v, i, ov, oi);
+            bad |= ob;
+        }
+    }
 };
+
+// The last workgroup of a launch to store its greedy partials combines all of them: wave 0 of
+// each workgroup, having stored its rows' partials (agent-scope atomics), waits for their
+// acknowledgements and counts the workgroup on `count`; in the workgroup that brings the count
+// to gridDim.x every wave then takes rows wave, wave + W, ..., reads their gridDim.x partials
+// (agent-scope atomic loads, issued only after the count) and writes each row's index, and
+// the count is reset for the next launch. The ordering is the split-K small-row reduction's
+// (waits and compiler barriers around agent-scope atomics), which avoids the cache-wide
+// write-back and invalidation of release/acquire. Called by every wave; `flag` is an LDS word.
+template <int W>
+__device__ __forceinline__ void greedy_last_group(const float *val, const int32_t *idx, int32_t *out,
+                                                  uint32_t *count, int M, int wave, int lane, int *flag) {
+    if (wave == 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        uint32_t old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if (lane == 0) *flag = old == gridDim.x - 1 ? 1 : 0;
+    }
+    lds_barrier();
+    if (__builtin_amdgcn_readfirstlane(*flag) == 0) return;
+    asm volatile("" ::: "memory");  // no partial read is moved above the count
+    const int G = (int)gridDim.x;
+    for (int m = wave; m < M; m += W) {
+        Greedy b = Greedy::none();
+        constexpr int kBatch = 8;
+        for (int c0 = 0; c0 < G; c0 += 64 * kBatch) {
+            float v[kBatch];
+            int i[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const int c = c0 + 64 * j + lane;
+                const size_t o = (size_t)m * G + (size_t)min(c, G - 1);
+                v[j] = __hip_atomic_load(val + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                i[j] = __hip_atomic_load(idx + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (c >= G) {  // past the row: a pair that never replaces a result
+                    v[j] = -__builtin_inff();
+                    i[j] = 0x7fffffff;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                if (i[j] < 0)
+                    b.bad = 1;
+                else
+                    better(b.v, b.i, v[j], i[j]);
+            }
+        }
+        b.wave64();
+        if (lane == 0) out[m] = b.bad ? -1 : b.i;
+    }
+    if (wave == 0 && lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Formats whose scale groups are 16 columns (Q6_K) run each 32-k step as MFMA rows of activation
 // rows masked to one half of the step: MFMA row 4q + 2a + h reads activation row q rpg + a (the
@@ -1539,8 +1608,11 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
             const int rpg = (p.M + 3) >> 2, g2 = lane / rpg, i2 = lane - g2 * rpg;
             Greedy b = red[g2 * 4 + i2];
             for (int w = 1; w < W; ++w) b.merge(red[(w * 4 + g2) * 4 + i2]);
-            b.write(p.amax_val, p.amax_idx, (size_t)lane * gridDim.x + blockIdx.x);
+            b.write_shared(p.amax_val, p.amax_idx, (size_t)lane * gridDim.x + blockIdx.x);
         }
+        // the word after the W x 16 entries, in the same unread partial slots
+        greedy_last_group<W>(p.amax_val, p.amax_idx, p.amax_out, p.amax_count, p.M, wave, lane,
+                             (int *)(red + W * 16));
     }
 }
 

@@ -31,10 +31,14 @@ struct QmmParams {
     // Tiled kernels: per input row, the factor that undoes the row's range scale (multiplied
     // into its outputs); null for none. The activations were then prescaled FP16 rows.
     const float *rscale;
-    // Greedy epilogue (persistent small-row kernels; GreedyArgs below)
+    // Greedy epilogue (persistent small-row kernels): as GemmParams' below, and the workgroup
+    // that finishes last combines every workgroup's partials into amax_out [M] (the rows'
+    // indices), counting arrivals on amax_count (zero between launches).
     float cap;
     float *amax_val;
     int32_t *amax_idx;
+    int32_t *amax_out;
+    uint32_t *amax_count;
 };
 
 // Decode probe: rows [row0, row0 + rows) of a weight matrix into [rows][K].
