@@ -117,3 +117,26 @@ def test_matmul_argmax_rejects_bad_arguments(gpu):
     for cap in (-1.0, float("inf"), float("nan")):
         with pytest.raises(jq.JvError, match="softcap"):
             jq.matmul_argmax(gpu, x, 1, w, out, cap, scratch)
+
+
+@pytest.mark.parametrize("act,m", [("f32", 3), ("f16", 20), ("bf16", 5), ("bf16", 24)])
+def test_matmul_argmax_other_activations_and_range(gpu, act, m):
+    """FP32 and FP16 activations, and BF16 rows beyond the FP16 range (divided by a power of
+    two before the FP16 rounding and multiplied back, kernels.rs:105, :120-130): the fused call
+    equals the three steps bit for bit, on the persistent kernels (M <= 16) and the 32 x 64
+    tiles."""
+    n, k = 32768, 512
+    raw = synth.weights(jq.Q6K, 12, n, k)
+    w = jq.QMatrix.upload(gpu, jq.Q6K, n, k, 1, raw)
+    x32 = synth.normal_rows(13, m, k)
+    if act == "bf16":
+        x32[1] *= np.float32(3e5)  # beyond 65504: this row takes a range factor
+    x, _ = activations(act, x32)
+    scratch = jq.SplitScratch(gpu)
+    for cap in (0.0, 30.0):
+        ref_out, ref_idx = _three_steps(gpu, x, m, w, n, cap, scratch)
+        out, idx = _fused(gpu, x, m, w, n, cap, scratch)
+        assert torch.equal(out, ref_out), cap
+        assert torch.equal(idx, ref_idx), cap
+        host = out.cpu().numpy()
+        assert [int(i) for i in idx.cpu()] == [_greedy_or_invalid(host[r]) for r in range(m)]
