@@ -356,6 +356,8 @@ def measure_configs(gpu, steps):
         out = torch.empty((m, n), dtype=torch.float32, device="cuda")
         jq.matmul(gpu, x, m, ms[0], out, scratch)
         jq.argmax_rows(gpu, out, scratch)
+        jq.matmul_argmax(gpu, x, m, ms[0], out, 30.0, scratch)  # its buffers grow before capture
+
         def three_steps(r):  # the reference's order: product, soft cap, greedy per row
             jq.matmul(gpu, x, m, ms[0], out, scratch)
             jq.softcap_logits(gpu, out, 30.0)

@@ -227,8 +227,11 @@ jv_status jv_argmax_rows(jv_ctx *ctx, const float *logits, size_t rows, size_t n
  * index[r] (device, m int32) = greedy's argmax of out row r (-1 for a row holding a non-finite
  * value). The results equal jv_matmul, jv_softcap_logits and jv_argmax_rows in turn. The
  * persistent small-row kernels and the Q4_K / Q6_K / Q8_0 register tiles (whole K) soft-cap
- * their outputs and leave each workgroup's per-row maximum in `scratch` as they store, so the
- * logits are not read again; other kernels are followed by the two other steps. m <= 65535. */
+ * their outputs and fold each row's maximum into a per-row key of the context as they store,
+ * and their last workgroup writes `index`, so the logits are not read again; other kernels are
+ * followed by the two other steps (which use `scratch`). The context's key buffer grows on the
+ * first call with more rows than before (run each row count once before graph capture).
+ * m <= 65535. */
 jv_status jv_matmul_argmax(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
                            const jv_qmatrix *w, float *out, size_t out_len, float cap, int32_t *index,
                            jv_scratch *scratch, void *stream);

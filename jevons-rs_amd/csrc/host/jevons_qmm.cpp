@@ -147,6 +147,10 @@ struct jv_ctx {
     void *pack = nullptr;  // packed activation fragments of the pipelined tiles (grows)
     size_t pack_bytes = 0;
     jv_scratch *own = nullptr;  // split-K small-row scratch of products given none (grows)
+    // greedy epilogue state of jv_matmul_argmax (grows, zeroed when allocated; each launch
+    // leaves what it used at zero): an arrival count, then per row a flag and a key
+    void *greedy = nullptr;
+    size_t greedy_rows = 0;
     // Buffers replaced by a larger one. A HIP graph captured before the growth still holds their
     // addresses, so they stay allocated until the context is closed.
     std::vector<void *> retired;
@@ -176,9 +180,6 @@ namespace {
 // allocated, a multiple of 16 after every launch); partial buffers of all uses follow them.
 constexpr size_t kCounterTiles = 65536;
 constexpr size_t kCounterBytes = kCounterTiles * 4;
-// The last counter is the greedy epilogue's arrival count (zero between launches); the split-K
-// small-row kernels take at most kCounterTiles - 1 tiles.
-constexpr size_t kGreedyCounter = kCounterTiles - 1;
 
 // Size of a grown buffer: at least twice the old one, so that the buffers a context retires
 // over its life add up to less than its largest one.
@@ -387,18 +388,16 @@ struct GroupArgs {
     uint32_t cap;
 };
 
-// The greedy epilogue asked of a product (jv_matmul_argmax): the soft cap and the scratch buffer
-// for the per-workgroup partials; the launch fills in where it put them and over how many
-// workgroup columns, or leaves `fused` false when the kernel it took has no such epilogue.
+// The greedy epilogue asked of a product (jv_matmul_argmax): the soft cap, the indices' buffer
+// and the context's greedy state; `done` tells whether the kernel the product took had the
+// epilogue (and so wrote the indices).
 struct GreedyArgs {
     float cap = 0.f;
-    jv_scratch *scratch = nullptr;
-    int32_t *index = nullptr;  // the rows' indices (written by the product when `done`)
-    float *val = nullptr;
-    int32_t *idx = nullptr;
-    int slots = 0;
-    bool fused = false;
-    bool done = false;  // the product's last workgroup combined the partials itself
+    int32_t *index = nullptr;
+    uint32_t *count = nullptr;
+    uint32_t *bad = nullptr;
+    uint64_t *key = nullptr;
+    bool done = false;
 };
 
 // jv_argmax_final over `rows` rows of `chunks` partials: one workgroup per row, of enough waves
@@ -410,12 +409,32 @@ jv_status launch_argmax_final(jv_ctx *ctx, float *pval, int32_t *pidx, int chunk
     return launch(ctx, "jv_argmax_final", dim3((unsigned)rows), dim3(threads), 0, stream, a2);
 }
 
-// Records the partials of `rows` x `slots` workgroup columns at `payload` (values, then indices).
-void greedy_partials(GreedyArgs *gr, size_t rows, int slots, void *payload) {
-    gr->val = (float *)payload;
-    gr->idx = (int32_t *)((uint8_t *)payload + rows * (size_t)slots * 4);
-    gr->slots = slots;
-    gr->fused = true;
+// The context's greedy state for at least `rows` rows, grown and zeroed as needed (a replaced
+// buffer is retired): the arrival count, padding to 256 bytes, a flag per row, then from the
+// next 256-byte boundary a key per row.
+size_t greedy_keys_at(size_t rows) { return 256 + ((rows * 4 + 255) & ~(size_t)255); }
+
+jv_status greedy_state(jv_ctx *ctx, size_t rows, GreedyArgs *gr) {
+    if (ctx->greedy_rows < rows) {
+        const size_t cap = std::max(rows, 2 * ctx->greedy_rows);
+        const size_t bytes = greedy_keys_at(cap) + cap * 8;
+        void *buf = nullptr;
+        JV_HIP(hipMalloc(&buf, bytes));
+        hipError_t e = hipMemset(buf, 0, bytes);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) {
+            hipFree(buf);
+            return fail(JV_ERR_HIP, "greedy state: %s", hipGetErrorString(e));
+        }
+        if (ctx->greedy) ctx->retired.push_back(ctx->greedy);
+        ctx->greedy = buf;
+        ctx->greedy_rows = cap;
+    }
+    uint8_t *base = (uint8_t *)ctx->greedy;
+    gr->count = (uint32_t *)base;
+    gr->bad = (uint32_t *)(base + 256);
+    gr->key = (uint64_t *)(base + greedy_keys_at(ctx->greedy_rows));
+    return JV_OK;
 }
 
 // Staging buffers of one product: `pack_bytes` of packed or converted activations (the context's
@@ -619,16 +638,16 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     const char *regenv = getenv("JV_GEMM_REG");
     const bool reg = reg_format(w) && (plan.bm == 32 || !(regenv && regenv[0] == '0'));
     const bool greedy = gr && !grp && plan.splits == 1 && reg && out_type == JV_OUT_F32;
-    const int slots = (int)(w->n / plan.bn);
     // fragments, then each packed row's range factor
     const size_t frag_bytes = (size_t)mtiles * 16 * w->k * 2;
-    const size_t part_bytes = plan.splits > 1 ? (size_t)plan.splits * m * w->n * 4
-                                              : (greedy ? m * (size_t)slots * 8 : 0);
+    const size_t part_bytes = plan.splits > 1 ? (size_t)plan.splits * m * w->n * 4 : 0;
     void *pack = nullptr, *partials = nullptr;
-    st = stage_buffers(ctx, greedy ? gr->scratch : scratch, frag_bytes + (size_t)mtiles * 16 * 4, part_bytes,
-                       &pack, &partials);
+    st = stage_buffers(ctx, scratch, frag_bytes + (size_t)mtiles * 16 * 4, part_bytes, &pack, &partials);
     if (st != JV_OK) return st;
-    if (greedy) greedy_partials(gr, m, slots, partials);
+    if (greedy) {
+        st = greedy_state(ctx, m, gr);
+        if (st != JV_OK) return st;
+    }
     float *rscale = (float *)((uint8_t *)pack + frag_bytes);
     st = launch_pack(ctx, x, act, m, w->k, mtiles, 0, (uint16_t *)pack, rscale, grp, plan.bm, stream);
     if (st != JV_OK) return st;
@@ -645,12 +664,14 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     gp.ldo = (int32_t)(w->n);
     gp.out_type = (int32_t)out_type;
     gp.splits = (int32_t)plan.splits;
+    gp.part = (float *)partials;
     if (greedy) {
         gp.cap = gr->cap;
-        gp.amax_val = gr->val;
-        gp.amax_idx = gr->idx;
-    } else {
-        gp.part = (float *)partials;
+        gp.amax_key = gr->key;
+        gp.amax_bad = gr->bad;
+        gp.amax_count = gr->count;
+        gp.amax_out = gr->index;
+        gr->done = true;
     }
     gp.split_stride = (int64_t)(m * w->n);
     if (grp) {
@@ -750,7 +771,7 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
         // split-K uses the context's own, so that its rows keep the bits of every other m.
         if (!scratch && lds_tile > lmax && !(wide && lds_persist <= lmax) && stage + 64 <= lmax)
             scratch = own_scratch(ctx);
-        const bool split_ok = scratch && U >= waves && (size_t)T <= kGreedyCounter && stage + 64 <= lmax;
+        const bool split_ok = scratch && U >= waves && (size_t)T <= kCounterTiles && stage + 64 <= lmax;
         // Persistent workgroups stage the activations once for several tiles: they serve wide
         // matrices and, above 2 rows, any matrix (at m = 4-8 on the decode shapes 10-34% faster
         // than the per-tile kernels, whose staging per tile or tile pair dominates there).
@@ -799,16 +820,13 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
                 JV_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 64 * waves, lds));
                 const int grid = std::min(T, cus * std::max(1, per_cu));
                 if (greedy) {
-                    void *payload = nullptr;
-                    st = scratch_reserve(gr->scratch, m * (size_t)grid * 8, &payload);
+                    st = greedy_state(ctx, m, gr);
                     if (st != JV_OK) return st;
-                    greedy_partials(gr, m, grid, payload);
                     p.cap = gr->cap;
-                    p.amax_val = gr->val;
-                    p.amax_idx = gr->idx;
-                    // the product's last workgroup writes the indices (no jv_argmax_final)
+                    p.amax_key = gr->key;
+                    p.amax_bad = gr->bad;
+                    p.amax_count = gr->count;
                     p.amax_out = gr->index;
-                    p.amax_count = (uint32_t *)gr->scratch->buf + kGreedyCounter;
                     gr->done = true;
                 }
                 return launch(ctx, name, dim3((unsigned)grid), dim3(64 * waves), lds, stream, args);
@@ -905,6 +923,7 @@ void jv_close(jv_ctx *ctx) {
     if (!ctx) return;
     hipSetDevice(ctx->device);
     if (ctx->pack) hipFree(ctx->pack);
+    if (ctx->greedy) hipFree(ctx->greedy);
     for (void *b : ctx->retired) hipFree(b);
     jv_scratch_free(ctx->own);
     if (ctx->module) hipModuleUnload(ctx->module);
@@ -1440,13 +1459,9 @@ jv_status jv_matmul_argmax(jv_ctx *ctx, const void *x, jv_act act, size_t x_len,
     const jv_plan plan = jv_plan_auto(w, m, 0);
     GreedyArgs gr;
     gr.cap = cap;
-    gr.scratch = scratch;
     gr.index = index;
     jv_status st = run_product(ctx, x, act, x_len, m, w, out, JV_OUT_F32, out_len, plan, scratch, stream, &gr);
     if (st != JV_OK || m == 0 || gr.done) return st;
-    if (gr.fused) {
-        return launch_argmax_final(ctx, gr.val, gr.idx, gr.slots, m, index, stream);
-    }
     if (cap > 0.f) {
         st = jv_softcap_logits(ctx, out, m * w->n, cap, stream);
         if (st != JV_OK) return st;

@@ -923,6 +923,16 @@ __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
 // The soft cap of one output value, the same expression as jv_softcap's; cap 0 leaves it.
 __device__ __forceinline__ float soft_capped(float v, float cap) { return cap > 0.f ? cap * tanhf(v / cap) : v; }
 
+// A (value, column) pair as one 64-bit key whose unsigned maximum is greedy's pick: the value's
+// bits mapped to an unsigned order (negative values inverted, positive ones with the sign bit
+// set), above the inverted column, so that equal values keep the lowest column. -0 is taken as
+// +0, which compares equal to it.
+__device__ __forceinline__ uint64_t greedy_key(float v, int col) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v == 0.f ? 0.f : v);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)ord << 32) | (uint64_t)(~(uint32_t)col);
+}
+
 // Largest value, its first column and whether any value was not finite, over the columns of one
 // output row that a lane (then a lane group, a wave, a workgroup) stores.
 struct Greedy {
@@ -949,79 +959,42 @@ struct Greedy {
             bad |= ob;
         }
     }
-    __device__ void write(float *val, int32_t *idx, size_t o) const {
-        val[o] = v;
-        idx[o] = bad ? -1 : i;
-    }
-    // the same as agent-scope atomic stores, for a reader in the same launch
-    __device__ void write_shared(float *val, int32_t *idx, size_t o) const {
-        __hip_atomic_store(val + o, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(idx + o, bad ? -1 : i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // over the 64 lanes of a wave
-    __device__ void wave64() {
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float ov = __shfl_xor(v, off);
-            const int oi = __shfl_xor(i, off);
-            const int ob = __shfl_xor(bad, off);
-            better(v, i, ov, oi);
-            bad |= ob;
-        }
+    // this row's result folded into its key or flag (agent-scope atomics, no return)
+    __device__ void fold(uint64_t *key, uint32_t *bad_row) const {
+        if (bad)
+            __hip_atomic_fetch_or(bad_row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            __hip_atomic_fetch_max(key, greedy_key(v, i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 };
 
-// The last workgroup of a launch to store its greedy partials combines all of them: wave 0 of
-// each workgroup, having stored its rows' partials (agent-scope atomics), waits for their
-// acknowledgements and counts the workgroup on `count`; in the workgroup that brings the count
-// to gridDim.x every wave then takes rows wave, wave + W, ..., reads their gridDim.x partials
-// (agent-scope atomic loads, issued only after the count) and writes each row's index, and
-// the count is reset for the next launch. The ordering is the split-K small-row reduction's
-// (waits and compiler barriers around agent-scope atomics), which avoids the cache-wide
-// write-back and invalidation of release/acquire. Called by every wave; `flag` is an LDS word.
-template <int W>
-__device__ __forceinline__ void greedy_last_group(const float *val, const int32_t *idx, int32_t *out,
-                                                  uint32_t *count, int M, int wave, int lane, int *flag) {
-    if (wave == 0) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        uint32_t old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        old = __builtin_amdgcn_readfirstlane(old);
-        if (lane == 0) *flag = old == gridDim.x - 1 ? 1 : 0;
+// The end of a greedy epilogue, after every thread has folded its rows (Greedy::fold): each
+// thread waits for its atomics' acknowledgements, the workgroup counts itself on p.amax_count,
+// and the workgroup that brings the count to the grid's size turns the M keys into columns
+// (-1 for flagged rows) and zeroes the keys, flags and count for the next launch. The atomics
+// are agent-scope (coherent across the XCDs) and ordered by the waits and compiler barriers,
+// as in the split-K small-row reduction, which avoids the cache-wide write-back and
+// invalidation of release/acquire. Called by every thread; `flag` is an LDS word.
+template <class P>
+__device__ __forceinline__ void greedy_last(const P &p, int *flag) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    const uint32_t groups = gridDim.x * gridDim.y * gridDim.z;
+    if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(p.amax_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = old == groups - 1 ? 1 : 0;
     }
     lds_barrier();
     if (__builtin_amdgcn_readfirstlane(*flag) == 0) return;
-    asm volatile("" ::: "memory");  // no partial read is moved above the count
-    const int G = (int)gridDim.x;
-    for (int m = wave; m < M; m += W) {
-        Greedy b = Greedy::none();
-        constexpr int kBatch = 8;
-        for (int c0 = 0; c0 < G; c0 += 64 * kBatch) {
-            float v[kBatch];
-            int i[kBatch];
-#pragma unroll
-            for (int j = 0; j < kBatch; ++j) {
-                const int c = c0 + 64 * j + lane;
-                const size_t o = (size_t)m * G + (size_t)min(c, G - 1);
-                v[j] = __hip_atomic_load(val + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                i[j] = __hip_atomic_load(idx + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (c >= G) {  // past the row: a pair that never replaces a result
-                    v[j] = -__builtin_inff();
-                    i[j] = 0x7fffffff;
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < kBatch; ++j) {
-                if (i[j] < 0)
-                    b.bad = 1;
-                else
-                    better(b.v, b.i, v[j], i[j]);
-            }
-        }
-        b.wave64();
-        if (lane == 0) out[m] = b.bad ? -1 : b.i;
+    asm volatile("" ::: "memory");  // no key is read before the count
+    for (int r = (int)threadIdx.x; r < p.M; r += (int)blockDim.x) {
+        const uint64_t k = __hip_atomic_load(p.amax_key + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t b = __hip_atomic_load(p.amax_bad + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        p.amax_out[r] = b ? -1 : (int32_t)~(uint32_t)k;
+        __hip_atomic_store(p.amax_key + r, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.amax_bad + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (wave == 0 && lane == 0) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(p.amax_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Formats whose scale groups are 16 columns (Q6_K) run each 32-k step as MFMA rows of activation
@@ -1608,11 +1581,10 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
             const int rpg = (p.M + 3) >> 2, g2 = lane / rpg, i2 = lane - g2 * rpg;
             Greedy b = red[g2 * 4 + i2];
             for (int w = 1; w < W; ++w) b.merge(red[(w * 4 + g2) * 4 + i2]);
-            b.write_shared(p.amax_val, p.amax_idx, (size_t)lane * gridDim.x + blockIdx.x);
+            b.fold(p.amax_key + lane, p.amax_bad + lane);
         }
         // the word after the W x 16 entries, in the same unread partial slots
-        greedy_last_group<W>(p.amax_val, p.amax_idx, p.amax_out, p.amax_count, p.M, wave, lane,
-                             (int *)(red + W * 16));
+        greedy_last(p, (int *)(red + W * 16));
     }
 }
 
@@ -2475,9 +2447,10 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
                 Greedy b = red[t * WN];
 #pragma unroll
                 for (int c = 1; c < WN; ++c) b.merge(red[t * WN + c]);
-                b.write(p.amax_val, p.amax_idx, (size_t)pr * gridDim.x + blockIdx.x);
+                b.fold(p.amax_key + pr, p.amax_bad + pr);
             }
         }
+        greedy_last(p, (int *)(red + 16 * TM * WN));  // the word after the entries
     }
 }
 
@@ -2617,8 +2590,9 @@ __device__ __forceinline__ void gemm8_body(const GemmParams &p) {
         if (t < 64 && pr < p.M) {
             Greedy b = red[2 * t];
             b.merge(red[2 * t + 1]);
-            b.write(p.amax_val, p.amax_idx, (size_t)pr * gridDim.x + blockIdx.x);
+            b.fold(p.amax_key + pr, p.amax_bad + pr);
         }
+        greedy_last(p, (int *)(red + 128));  // the word after the entries
     }
 }
 

@@ -31,14 +31,12 @@ struct QmmParams {
     // Tiled kernels: per input row, the factor that undoes the row's range scale (multiplied
     // into its outputs); null for none. The activations were then prescaled FP16 rows.
     const float *rscale;
-    // Greedy epilogue (persistent small-row kernels): as GemmParams' below, and the workgroup
-    // that finishes last combines every workgroup's partials into amax_out [M] (the rows'
-    // indices), counting arrivals on amax_count (zero between launches).
+    // Greedy epilogue (persistent small-row kernels): as GemmParams' below.
     float cap;
-    float *amax_val;
-    int32_t *amax_idx;
-    int32_t *amax_out;
+    uint64_t *amax_key;
+    uint32_t *amax_bad;
     uint32_t *amax_count;
+    int32_t *amax_out;
 };
 
 // Decode probe: rows [row0, row0 + rows) of a weight matrix into [rows][K].
@@ -90,14 +88,18 @@ struct GemmParams {
     float *part;
     int64_t split_stride;
     int32_t splits;
-    // Greedy epilogue (ungrouped, whole K, FP32 outputs): with amax_val set, every output value
-    // is first soft-capped, cap tanh(v / cap), when cap > 0, then stored, and each workgroup
-    // writes, per output row it covers, the largest of its columns' values and that value's
-    // first column to amax_val / amax_idx [M][gridDim.x] at column blockIdx.x (index -1 when
-    // one of the values is not finite). The same fields close QmmParams.
+    // Greedy epilogue (ungrouped, whole K, FP32 outputs), in the kernels built with it: every
+    // output value is soft-capped, cap tanh(v / cap), when cap > 0, then stored, and each
+    // workgroup folds, per output row it covers, the largest of its columns' values and that
+    // value's first column into amax_key[row] (an atomic maximum of the ordered value bits over
+    // the inverted column) or sets amax_bad[row] when one of its values is not finite; the
+    // workgroup that counts last on amax_count writes amax_out[row] (the column, -1 for a bad
+    // row) and zeroes the keys, flags and count it used. All three start at zero.
     float cap;
-    float *amax_val;
-    int32_t *amax_idx;
+    uint64_t *amax_key;
+    uint32_t *amax_bad;
+    uint32_t *amax_count;
+    int32_t *amax_out;
 };
 
 // GGML blocks (device copy of the upload) -> device layout.
