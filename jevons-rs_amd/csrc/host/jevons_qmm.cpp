@@ -669,9 +669,6 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
         gp.cap = gr->cap;
         gp.amax_key = gr->key;
         gp.amax_bad = gr->bad;
-        gp.amax_count = gr->count;
-        gp.amax_out = gr->index;
-        gr->done = true;
     }
     gp.split_stride = (int64_t)(m * w->n);
     if (grp) {
@@ -695,6 +692,14 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     const size_t glds = 4 * ((reg ? 0 : plan.bm) + plan.bn) / 16 * 1024;
     st = launch(ctx, name, dim3((unsigned)(w->n / plan.bn), (unsigned)jobs_or_tiles, plan.splits),
                 dim3(64 * waves), glds, stream, gargs);
+    if (st == JV_OK && greedy) {  // the rows' columns from the keys the tiles folded
+        int32_t *index = gr->index;
+        int rows = (int)m;
+        void *fargs[] = {&gr->key, &gr->bad, &index, &rows};
+        st = launch(ctx, "jv_greedy_finish", dim3((unsigned)((m + 255) / 256)), dim3(256), 0, stream, fargs);
+        if (st == JV_OK) gr->done = true;
+        return st;
+    }
     if (st != JV_OK || plan.splits == 1) return st;
     const void *part = partials;
     int64_t len = (int64_t)(m * w->n);

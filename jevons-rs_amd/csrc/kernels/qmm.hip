@@ -997,6 +997,19 @@ __device__ __forceinline__ void greedy_last(const P &p, int *flag) {
     if (threadIdx.x == 0) __hip_atomic_store(p.amax_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// After a product whose workgroups folded their rows into the greedy keys without counting (the
+// tiles' epilogue): each row's column (-1 for a flagged row), and the keys and flags zeroed for
+// the next launch. Grid: ceil(M / 256) x 256 threads.
+extern "C" __global__ __launch_bounds__(256) void jv_greedy_finish(uint64_t *key, uint32_t *bad, int32_t *out,
+                                                                  int M) {
+    const int r = (int)(blockIdx.x * 256 + threadIdx.x);
+    if (r >= M) return;
+    const uint64_t k = key[r];
+    out[r] = bad[r] ? -1 : (int32_t)~(uint32_t)k;
+    key[r] = 0;
+    bad[r] = 0;
+}
+
 // Formats whose scale groups are 16 columns (Q6_K) run each 32-k step as MFMA rows of activation
 // rows masked to one half of the step: MFMA row 4q + 2a + h reads activation row q rpg + a (the
 // row of accumulator element a of lane group q) in lane groups 2h, 2h + 1 and the zero row in
@@ -2410,8 +2423,9 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
                     const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
                     const float v = acc[i][k][e] * p.rscale[pr];  // exact: a power of two
                     if constexpr (GR) {  // ungrouped, whole K, FP32 outputs (the host's rule)
+                        // kept in place and stored after the count (below)
                         const float c = soft_capped(v, p.cap);
-                        ((float *)p.out)[o] = c;
+                        acc[i][k][e] = c;
                         gr[i][e].add(c, col);
                     } else if (p.splits > 1) {
                         p.part[(int64_t)blockIdx.z * p.split_stride + (int64_t)o] = v;
@@ -2450,7 +2464,19 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
                 b.fold(p.amax_key + pr, p.amax_bad + pr);
             }
         }
-        greedy_last(p, (int *)(red + 16 * TM * WN));  // the word after the entries
+        // no wait and no count: the keys are read by jv_greedy_finish after the launch
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+#pragma unroll
+            for (int k = 0; k < NT; ++k) {
+                const int col = (t0 + n_of(k)) * 16 + r;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = (mt0 + m_of(i)) * 16 + 4 * g + e;
+                    if (m < p.M) ((float *)p.out)[(size_t)m * (size_t)p.ldo + (size_t)col] = acc[i][k][e];
+                }
+            }
+        }
     }
 }
 
@@ -2561,8 +2587,9 @@ __device__ __forceinline__ void gemm8_body(const GemmParams &p) {
                 const size_t o = (size_t)m * (size_t)p.ldo + (size_t)col;
                 const float v = acc[k][e] * p.rscale[m];  // exact: a power of two
                 if constexpr (GR) {  // ungrouped, whole K, FP32 outputs (the host's rule)
+                    // kept in place and stored after the count (below)
                     const float c = soft_capped(v, p.cap);
-                    ((float *)p.out)[o] = c;
+                    acc[k][e] = c;
                     gr[e].add(c, col);
                 } else if (p.splits > 1) {
                     p.part[(int64_t)blockIdx.z * p.split_stride + (int64_t)o] = v;
@@ -2592,7 +2619,16 @@ __device__ __forceinline__ void gemm8_body(const GemmParams &p) {
             b.merge(red[2 * t + 1]);
             b.fold(p.amax_key + pr, p.amax_bad + pr);
         }
-        greedy_last(p, (int *)(red + 128));  // the word after the entries
+        // no wait and no count: the keys are read by jv_greedy_finish after the launch
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int col = (t0 + 2 * nh + k) * 16 + r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = (mt0 + mq) * 16 + 4 * g + e;
+                if (m < p.M) ((float *)p.out)[(size_t)m * (size_t)p.ldo + (size_t)col] = acc[k][e];
+            }
+        }
     }
 }
 

@@ -92,9 +92,11 @@ struct GemmParams {
     // output value is soft-capped, cap tanh(v / cap), when cap > 0, then stored, and each
     // workgroup folds, per output row it covers, the largest of its columns' values and that
     // value's first column into amax_key[row] (an atomic maximum of the ordered value bits over
-    // the inverted column) or sets amax_bad[row] when one of its values is not finite; the
-    // workgroup that counts last on amax_count writes amax_out[row] (the column, -1 for a bad
-    // row) and zeroes the keys, flags and count it used. All three start at zero.
+    // the inverted column) or sets amax_bad[row] when one of its values is not finite. In the
+    // persistent small-row kernels the workgroup that counts last on amax_count writes
+    // amax_out[row] (the column, -1 for a bad row) and zeroes the keys, flags and count it used;
+    // after the tiles jv_greedy_finish does that (the tiles leave amax_count and amax_out
+    // unused). All three start at zero.
     float cap;
     uint64_t *amax_key;
     uint32_t *amax_bad;
