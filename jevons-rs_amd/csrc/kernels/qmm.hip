@@ -920,8 +920,31 @@ __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
     }
 }
 
-// The soft cap of one output value, the same expression as jv_softcap's; cap 0 leaves it.
-__device__ __forceinline__ float soft_capped(float v, float cap) { return cap > 0.f ? cap * tanhf(v / cap) : v; }
+// tanh for the soft cap, odd: below |y| = 0.625 the series form y + y^3 Q(y^2), with Q of
+// degree 5 fitted by least squares here to (tanh y / y - 1) / y^2 on [0, 0.625^2] (fit error
+// 5e-9 relative); above, tanh |y| = 1 - 2 / (e^(2|y|) + 1) through the hardware 2^x and
+// reciprocal (e^(2|y|) = 2^(2 log2(e) |y|)). Within 2 ulp of tanh in float32 simulation and
+// a few ulp on the device (the tests hold it to 6), at a third of the library call's
+// instructions. +-inf give +-1, NaN stays NaN.
+__device__ __forceinline__ float cap_tanh(float y) {
+    const float a = __builtin_fabsf(y), t = y * y;
+    float q = 1.618547598e-03f;
+    q = __builtin_fmaf(q, t, -7.621073630e-03f);
+    q = __builtin_fmaf(q, t, 2.148471028e-02f);
+    q = __builtin_fmaf(q, t, -5.390961096e-02f);
+    q = __builtin_fmaf(q, t, 1.333293766e-01f);
+    q = __builtin_fmaf(q, t, -3.333332539e-01f);
+    const float small = __builtin_fmaf(y * t, q, y);
+    const float e = __builtin_amdgcn_exp2f(a * 2.885390082f);
+    const float big = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+    return a < 0.625f ? small : __builtin_copysignf(big, y);
+}
+
+// The soft cap of one output value, cap tanh(v / cap), the same expression in jv_softcap and in
+// the greedy epilogue; cap 0 leaves it.
+__device__ __forceinline__ float soft_capped(float v, float cap) {
+    return cap > 0.f ? cap * cap_tanh(v * (1.0f / cap)) : v;
+}
 
 // A (value, column) pair as one 64-bit key whose unsigned maximum is greedy's pick: the value's
 // bits mapped to an unsigned order (negative values inverted, positive ones with the sign bit

@@ -140,3 +140,28 @@ def test_matmul_argmax_other_activations_and_range(gpu, act, m):
         assert torch.equal(idx, ref_idx), cap
         host = out.cpu().numpy()
         assert [int(i) for i in idx.cpu()] == [_greedy_or_invalid(host[r]) for r in range(m)]
+
+
+@pytest.mark.parametrize("cap", [30.0, 1.0, 0.125])
+def test_softcap_tanh_accuracy(gpu, cap):
+    """The soft cap's tanh (a fitted series below |y| = 0.625, 1 - 2 / (e^(2|y|) + 1) above)
+    within 6 ulp of cap tanh(v / cap) computed in f64, over a dense sweep of v / cap in
+    [-12, 12] (both branches, the switch point, saturation), tiny and zero values, and +-inf;
+    NaN stays NaN."""
+    rng = np.random.default_rng(5)
+    y = np.concatenate([np.linspace(-12, 12, 2000001), np.linspace(-0.7, 0.7, 400001),
+                        np.array([0.625, -0.625, np.nextafter(0.625, 0), 1e-30, -1e-30, 0.0, -0.0, 60.0, -60.0]),
+                        rng.standard_normal(100000) * 3]).astype(np.float32)
+    v = (y.astype(np.float64) * cap).astype(np.float32)
+    t = torch.from_numpy(v.copy()).cuda()
+    jq.softcap_logits(gpu, t, cap)
+    got = t.cpu().numpy().astype(np.float64)
+    want = cap * np.tanh(v.astype(np.float64) / cap)
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    err = np.abs(got - want) / np.maximum(ulp, np.spacing(np.float32(0)))
+    say("cap", cap, "max ulp", float(err.max()))
+    assert err.max() <= 6.0
+    special = torch.tensor([np.inf, -np.inf, np.nan], dtype=torch.float32, device="cuda")
+    jq.softcap_logits(gpu, special, cap)
+    s = special.cpu().numpy()
+    assert s[0] == np.float32(cap) and s[1] == -np.float32(cap) and np.isnan(s[2])
