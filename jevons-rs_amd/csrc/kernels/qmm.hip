@@ -921,8 +921,8 @@ __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
 }
 
 // tanh for the soft cap, odd: below |y| = 0.625 the series form y + y^3 Q(y^2), with Q of
-// degree 5 fitted by least squares here to (tanh y / y - 1) / y^2 on [0, 0.625^2] (fit error
-// 5e-9 relative); above, tanh |y| = 1 - 2 / (e^(2|y|) + 1) through the hardware 2^x and
+// degree 5 fitted by least squares to (tanh y / y - 1) / y^2 on [0, 0.625^2] (fit error 5e-9
+// relative; softcap_tanh_fit.py beside this file recomputes it); above, tanh |y| = 1 - 2 / (e^(2|y|) + 1) through the hardware 2^x and
 // reciprocal (e^(2|y|) = 2^(2 log2(e) |y|)). Within 2 ulp of tanh in float32 simulation and
 // a few ulp on the device (the tests hold it to 6), at a third of the library call's
 // instructions. +-inf give +-1, NaN stays NaN.
