@@ -1455,7 +1455,7 @@ jv_status jv_matmul_argmax(jv_ctx *ctx, const void *x, jv_act act, size_t x_len,
     if (!w) return fail(JV_ERR_INVALID, "null weight matrix");
     if (!(cap >= 0.f) || !std::isfinite(cap))
         return fail(JV_ERR_INVALID, "softcap %g must be 0 (none) or positive", (double)cap);
-    if (!index) return fail(JV_ERR_INVALID, "null index buffer");
+    if (!index && m > 0) return fail(JV_ERR_INVALID, "null index buffer");
     if (!scratch) return fail(JV_ERR_INVALID, "argmax needs a scratch buffer");
     if (m > 65535 || w->n > (size_t)INT32_MAX)
         return fail(JV_ERR_INVALID, "argmax of %zu rows x %zu is too large", m, w->n);

@@ -165,3 +165,23 @@ def test_softcap_tanh_accuracy(gpu, cap):
     jq.softcap_logits(gpu, special, cap)
     s = special.cpu().numpy()
     assert s[0] == np.float32(cap) and s[1] == -np.float32(cap) and np.isnan(s[2])
+
+
+@pytest.mark.parametrize("kind,m", [(jq.Q5_0, 20), (jq.Q5_0, 1), (jq.Q4K, 0)])
+def test_matmul_argmax_without_epilogue_kernels(gpu, kind, m):
+    """Formats without the epilogue variants (Q5_0 runs the generic kernels) take the three
+    steps with the same results; M = 0 does nothing."""
+    n, k = 4096, 512
+    raw = synth.weights(kind, 14, n, k)
+    w = jq.QMatrix.upload(gpu, kind, n, k, 1, raw)
+    if m == 0:
+        x = torch.zeros((1, k), dtype=torch.bfloat16, device="cuda")
+        out = torch.zeros((1, n), dtype=torch.float32, device="cuda")
+        assert jq.matmul_argmax(gpu, x, 0, w, out, 30.0, jq.SplitScratch(gpu)).numel() == 0
+        return
+    x, _ = activations("bf16", synth.normal_rows(15, m, k))
+    scratch = jq.SplitScratch(gpu)
+    for cap in (0.0, 30.0):
+        ref_out, ref_idx = _three_steps(gpu, x, m, w, n, cap, scratch)
+        out, idx = _fused(gpu, x, m, w, n, cap, scratch)
+        assert torch.equal(out, ref_out) and torch.equal(idx, ref_idx), cap
