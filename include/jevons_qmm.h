@@ -228,7 +228,8 @@ jv_status jv_argmax_rows(jv_ctx *ctx, const float *logits, size_t rows, size_t n
  * value). The results equal jv_matmul, jv_softcap_logits and jv_argmax_rows in turn. The
  * persistent small-row kernels and the Q4_K / Q6_K / Q8_0 register tiles (whole K) soft-cap
  * their outputs and fold each row's maximum into a per-row key of the context as they store,
- * and their last workgroup writes `index`, so the logits are not read again; other kernels are
+ * and a small second launch writes `index` from the keys, so the logits are not read again;
+ * other kernels are
  * followed by the two other steps (which use `scratch`). The context's key buffer grows on the
  * first call with more rows than before (run each row count once before graph capture).
  * m <= 65535. */

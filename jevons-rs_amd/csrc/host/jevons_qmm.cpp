@@ -147,8 +147,8 @@ struct jv_ctx {
     void *pack = nullptr;  // packed activation fragments of the pipelined tiles (grows)
     size_t pack_bytes = 0;
     jv_scratch *own = nullptr;  // split-K small-row scratch of products given none (grows)
-    // greedy epilogue state of jv_matmul_argmax (grows, zeroed when allocated; each launch
-    // leaves what it used at zero): an arrival count, then per row a flag and a key
+    // greedy epilogue state of jv_matmul_argmax (grows, zeroed when allocated; each call
+    // leaves what it used at zero): per row a flag and a key
     void *greedy = nullptr;
     size_t greedy_rows = 0;
     // Buffers replaced by a larger one. A HIP graph captured before the growth still holds their
@@ -394,7 +394,6 @@ struct GroupArgs {
 struct GreedyArgs {
     float cap = 0.f;
     int32_t *index = nullptr;
-    uint32_t *count = nullptr;
     uint32_t *bad = nullptr;
     uint64_t *key = nullptr;
     bool done = false;
@@ -410,9 +409,8 @@ jv_status launch_argmax_final(jv_ctx *ctx, float *pval, int32_t *pidx, int chunk
 }
 
 // The context's greedy state for at least `rows` rows, grown and zeroed as needed (a replaced
-// buffer is retired): the arrival count, padding to 256 bytes, a flag per row, then from the
-// next 256-byte boundary a key per row.
-size_t greedy_keys_at(size_t rows) { return 256 + ((rows * 4 + 255) & ~(size_t)255); }
+// buffer is retired): a flag per row, then from the next 256-byte boundary a key per row.
+size_t greedy_keys_at(size_t rows) { return (rows * 4 + 255) & ~(size_t)255; }
 
 jv_status greedy_state(jv_ctx *ctx, size_t rows, GreedyArgs *gr) {
     if (ctx->greedy_rows < rows) {
@@ -431,10 +429,20 @@ jv_status greedy_state(jv_ctx *ctx, size_t rows, GreedyArgs *gr) {
         ctx->greedy_rows = cap;
     }
     uint8_t *base = (uint8_t *)ctx->greedy;
-    gr->count = (uint32_t *)base;
-    gr->bad = (uint32_t *)(base + 256);
+    gr->bad = (uint32_t *)base;
     gr->key = (uint64_t *)(base + greedy_keys_at(ctx->greedy_rows));
     return JV_OK;
+}
+
+// After a product with the greedy epilogue: jv_greedy_finish turns the folded keys of its `rows`
+// rows into gr->index and zeroes them.
+jv_status greedy_finish(jv_ctx *ctx, GreedyArgs *gr, size_t rows, void *stream) {
+    int32_t *index = gr->index;
+    int r = (int)rows;
+    void *args[] = {&gr->key, &gr->bad, &index, &r};
+    jv_status st = launch(ctx, "jv_greedy_finish", dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, args);
+    if (st == JV_OK) gr->done = true;
+    return st;
 }
 
 // Staging buffers of one product: `pack_bytes` of packed or converted activations (the context's
@@ -692,14 +700,7 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     const size_t glds = 4 * ((reg ? 0 : plan.bm) + plan.bn) / 16 * 1024;
     st = launch(ctx, name, dim3((unsigned)(w->n / plan.bn), (unsigned)jobs_or_tiles, plan.splits),
                 dim3(64 * waves), glds, stream, gargs);
-    if (st == JV_OK && greedy) {  // the rows' columns from the keys the tiles folded
-        int32_t *index = gr->index;
-        int rows = (int)m;
-        void *fargs[] = {&gr->key, &gr->bad, &index, &rows};
-        st = launch(ctx, "jv_greedy_finish", dim3((unsigned)((m + 255) / 256)), dim3(256), 0, stream, fargs);
-        if (st == JV_OK) gr->done = true;
-        return st;
-    }
+    if (st == JV_OK && greedy) return greedy_finish(ctx, gr, m, stream);
     if (st != JV_OK || plan.splits == 1) return st;
     const void *part = partials;
     int64_t len = (int64_t)(m * w->n);
@@ -830,11 +831,9 @@ jv_status run_product(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size
                     p.cap = gr->cap;
                     p.amax_key = gr->key;
                     p.amax_bad = gr->bad;
-                    p.amax_count = gr->count;
-                    p.amax_out = gr->index;
-                    gr->done = true;
                 }
-                return launch(ctx, name, dim3((unsigned)grid), dim3(64 * waves), lds, stream, args);
+                st = launch(ctx, name, dim3((unsigned)grid), dim3(64 * waves), lds, stream, args);
+                return st == JV_OK && greedy ? greedy_finish(ctx, gr, m, stream) : st;
             }
             snprintf(name, sizeof name, "jv_qmv_%s_t%d_m%d", fname, tw, mv);
             return launch(ctx, name, dim3((unsigned)((T + tw - 1) / tw)), dim3(64 * waves), lds, stream, args);

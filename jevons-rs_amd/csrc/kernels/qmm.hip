@@ -991,38 +991,9 @@ struct Greedy {
     }
 };
 
-// The end of a greedy epilogue, after every thread has folded its rows (Greedy::fold): each
-// thread waits for its atomics' acknowledgements, the workgroup counts itself on p.amax_count,
-// and the workgroup that brings the count to the grid's size turns the M keys into columns
-// (-1 for flagged rows) and zeroes the keys, flags and count for the next launch. The atomics
-// are agent-scope (coherent across the XCDs) and ordered by the waits and compiler barriers,
-// as in the split-K small-row reduction, which avoids the cache-wide write-back and
-// invalidation of release/acquire. Called by every thread; `flag` is an LDS word.
-template <class P>
-__device__ __forceinline__ void greedy_last(const P &p, int *flag) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    lds_barrier();
-    const uint32_t groups = gridDim.x * gridDim.y * gridDim.z;
-    if (threadIdx.x == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(p.amax_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = old == groups - 1 ? 1 : 0;
-    }
-    lds_barrier();
-    if (__builtin_amdgcn_readfirstlane(*flag) == 0) return;
-    asm volatile("" ::: "memory");  // no key is read before the count
-    for (int r = (int)threadIdx.x; r < p.M; r += (int)blockDim.x) {
-        const uint64_t k = __hip_atomic_load(p.amax_key + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t b = __hip_atomic_load(p.amax_bad + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        p.amax_out[r] = b ? -1 : (int32_t)~(uint32_t)k;
-        __hip_atomic_store(p.amax_key + r, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.amax_bad + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(p.amax_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// After a product whose workgroups folded their rows into the greedy keys without counting (the
-// tiles' epilogue): each row's column (-1 for a flagged row), and the keys and flags zeroed for
-// the next launch. Grid: ceil(M / 256) x 256 threads.
+// After a product whose workgroups folded their rows into the greedy keys (Greedy::fold): each
+// row's column (-1 for a flagged row), and the keys and flags zeroed for the next launch. Grid:
+// ceil(M / 256) x 256 threads.
 extern "C" __global__ __launch_bounds__(256) void jv_greedy_finish(uint64_t *key, uint32_t *bad, int32_t *out,
                                                                   int M) {
     const int r = (int)(blockIdx.x * 256 + threadIdx.x);
@@ -1619,8 +1590,6 @@ __device__ __forceinline__ void qmvp_body(const QmmParams &p) {
             for (int w = 1; w < W; ++w) b.merge(red[(w * 4 + g2) * 4 + i2]);
             b.fold(p.amax_key + lane, p.amax_bad + lane);
         }
-        // the word after the W x 16 entries, in the same unread partial slots
-        greedy_last(p, (int *)(red + W * 16));
     }
 }
 
@@ -2487,7 +2456,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams &p) {
                 b.fold(p.amax_key + pr, p.amax_bad + pr);
             }
         }
-        // no wait and no count: the keys are read by jv_greedy_finish after the launch
+        // no wait: the keys are read by jv_greedy_finish after the launch
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
 #pragma unroll
@@ -2642,7 +2611,7 @@ __device__ __forceinline__ void gemm8_body(const GemmParams &p) {
             b.merge(red[2 * t + 1]);
             b.fold(p.amax_key + pr, p.amax_bad + pr);
         }
-        // no wait and no count: the keys are read by jv_greedy_finish after the launch
+        // no wait: the keys are read by jv_greedy_finish after the launch
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const int col = (t0 + 2 * nh + k) * 16 + r;

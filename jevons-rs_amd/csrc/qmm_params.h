@@ -35,8 +35,6 @@ struct QmmParams {
     float cap;
     uint64_t *amax_key;
     uint32_t *amax_bad;
-    uint32_t *amax_count;
-    int32_t *amax_out;
 };
 
 // Decode probe: rows [row0, row0 + rows) of a weight matrix into [rows][K].
@@ -92,16 +90,12 @@ struct GemmParams {
     // output value is soft-capped, cap tanh(v / cap), when cap > 0, then stored, and each
     // workgroup folds, per output row it covers, the largest of its columns' values and that
     // value's first column into amax_key[row] (an atomic maximum of the ordered value bits over
-    // the inverted column) or sets amax_bad[row] when one of its values is not finite. In the
-    // persistent small-row kernels the workgroup that counts last on amax_count writes
-    // amax_out[row] (the column, -1 for a bad row) and zeroes the keys, flags and count it used;
-    // after the tiles jv_greedy_finish does that (the tiles leave amax_count and amax_out
-    // unused). All three start at zero.
+    // the inverted column) or sets amax_bad[row] when one of its values is not finite; both start
+    // at zero, and jv_greedy_finish, launched after the product, turns them into the rows'
+    // columns and zeroes them again.
     float cap;
     uint64_t *amax_key;
     uint32_t *amax_bad;
-    uint32_t *amax_count;
-    int32_t *amax_out;
 };
 
 // GGML blocks (device copy of the upload) -> device layout.
