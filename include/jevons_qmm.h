@@ -229,9 +229,9 @@ jv_status jv_argmax_rows(jv_ctx *ctx, const float *logits, size_t rows, size_t n
  * persistent small-row kernels and the Q4_K / Q6_K / Q8_0 register tiles (whole K) soft-cap
  * their outputs and fold each row's maximum into a per-row key of the context as they store,
  * and a small second launch writes `index` from the keys, so the logits are not read again;
- * other kernels are
- * followed by the two other steps (which use `scratch`). The context's key buffer grows on the
- * first call with more rows than before (run each row count once before graph capture).
+ * other kernels are followed by the two other steps (which use `scratch`). The context's key
+ * buffer grows on the first call with more rows than before (run each row count once before
+ * graph capture), and calls on one context must not run concurrently (they share the keys).
  * m <= 65535. */
 jv_status jv_matmul_argmax(jv_ctx *ctx, const void *x, jv_act act, size_t x_len, size_t m,
                            const jv_qmatrix *w, float *out, size_t out_len, float cap, int32_t *index,
