@@ -1949,7 +1949,7 @@ __device__ __forceinline__ f16x8 act8_cvt(const u32x4 r[2], float s) {
 //    whose largest magnitude exceeds 16384 (crates/jevons-burn/src/kernels.rs:105, :120-130),
 //    so the division is exact; 1 otherwise.
 // rscale[R] receives each packed (or row-major) row's factor, for the product to multiply its
-// outputs by; rows of padding pack zeros with factor 1, and unused job slots are skipped.
+// outputs by; rows of padding and unused job slots are skipped.
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ uint16_t *frag_dst(const PackXParams &p, int R, int c) {
     // chunk c (k = 8 c) of packed row R: fragment (mt U + u) 8 + s, lane 16 g + r
@@ -2038,14 +2038,12 @@ __device__ __forceinline__ void pack_rows(const PackXParams &p) {
         mx = __builtin_fmaxf(mx, wmax[w][rr]);
         inf |= wnf[w][rr];
     }
-    if (xr == -2) return;  // past the rows, or an unused job slot: nothing is read from it
+    // Rows of padding (past M, or past a job's rows) and unused job slots are not written: the
+    // products compute those rows from whatever the buffer holds and store none of them (an
+    // output row depends on its own activation row only).
+    if (xr < 0) return;
     float f;
     const float s = range_scale(inf ? __builtin_inff() : mx, &f);
-    if (xr < 0) {
-        for (int c = cl; c < chunks; c += tpr) *(u32x4 *)frag_dst(p, R, c) = u32x4{0u, 0u, 0u, 0u};
-        if (cl == 0) p.rscale[R] = 1.f;
-        return;
-    }
     for (int c0 = 0; c0 < chunks; c0 += tpr * B) {
         if (!held) load_batch(c0);  // longer rows: read the batch again (from the cache)
 #pragma unroll
@@ -2067,15 +2065,13 @@ __device__ __forceinline__ void pack_copy(const PackXParams &p) {
     const int64_t mu = q >> 1;
     const int R = (int)(mu / U) * 16 + (lane & 15);  // packed row
     const int row = packed_source(p, R);
-    if (row == -2) return;
+    if (row < 0) return;  // padding or an unused job slot: not written (pack_rows)
     const int col0 = (int)(mu % U) * 256 + half * 128 + (lane >> 4) * 8;
     uint16_t *dst = p.out + ((mu * 8 + 4 * half) * 64 + lane) * 8;
-    u32x4 h[4] = {};
-    if (row >= 0) {
+    u32x4 h[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-            h[s] = *(const u32x4 *)((const uint16_t *)p.x + (size_t)row * (size_t)p.ldx + (size_t)(col0 + 32 * s));
-    }
+    for (int s = 0; s < 4; ++s)
+        h[s] = *(const u32x4 *)((const uint16_t *)p.x + (size_t)row * (size_t)p.ldx + (size_t)(col0 + 32 * s));
     if (mu % U == 0 && half == 0 && lane < 16) p.rscale[R] = 1.f;
 #pragma unroll
     for (int s = 0; s < 4; ++s) *(u32x4 *)(dst + s * 512) = h[s];

@@ -49,7 +49,8 @@ struct DequantParams {
 };
 
 // Activation rows -> FP16 MFMA A fragments of 1 KB: fragment (mt * U + u) * 8 + s (U = K / 256)
-// holds, for lane 16g + r, x[16 mt + r][256 u + 32 s + 8 g + e], e < 8; rows >= M are zero.
+// holds, for lane 16g + r, x[16 mt + r][256 u + 32 s + 8 g + e], e < 8; rows >= M (and a job's
+// rows past its count) are not written, and no product stores their outputs.
 // Rows of BF16 or FP32 values above 16384 are divided by a power-of-two range factor first;
 // rscale[R] gets packed row R's factor, for the product to undo. With `rowmajor` (BF16 and
 // FP32 only, never grouped) the output is FP16 rows [M][K] and rscale per row.
