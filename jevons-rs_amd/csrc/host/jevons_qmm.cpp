@@ -691,9 +691,17 @@ jv_status launch_pipelined(jv_ctx *ctx, const void *x, jv_act act, size_t m, con
     // Q4_K, Q6_K and Q8_0 tiles run on waves that keep their activation fragments in
     // registers (same bits as the tiles that share them through LDS; JV_GEMM_REG=0 selects
     // those, except for 32 x 64, which exists only with register fragments): `reg` above.
-    // Ungrouped 64 x 64 products run the 8-wave tile (two waves per SIMD); expert jobs keep the
-    // 4-wave one, faster there.
-    const bool w8 = reg && !grp && plan.bm == 64;
+    // Ungrouped 64 x 64 products run the 8-wave tile (two waves per SIMD) up to two workgroups
+    // per CU; larger grids and expert jobs the 4-wave one, whose waves issue their MFMAs at
+    // raised priority, several workgroups per CU (fused q/k/v at 256 rows, 512 workgroups:
+    // 40.0 against 43.9 us; q and o, 240-256 workgroups: 0.3-0.6 us slower on it). The two
+    // give the same bits; only the 8-wave tile has the greedy epilogue. JV_GEMM_W8=0 / 1
+    // forces one (tests, tuning).
+    const char *w8env = getenv("JV_GEMM_W8");
+    const size_t blocks = (w->n / plan.bn) * (size_t)jobs_or_tiles * plan.splits;
+    const bool few = blocks < 2 * (size_t)std::max(1, ctx->info.compute_units);
+    const bool w8 = reg && !grp && plan.bm == 64 &&
+                    (greedy || (w8env ? w8env[0] != '0' : few));
     snprintf(name, sizeof name, "jv_gemm_%s_%ux%u%s%s", fmt_kernel_name(w->fmt), plan.bm, plan.bn,
              w8 ? "r8" : (reg ? "r" : ""), greedy ? "_g" : "");
     const unsigned waves = plan.bm >= 128 || w8 ? 8 : 4;

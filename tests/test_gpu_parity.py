@@ -403,8 +403,8 @@ def test_register_activation_tiles_equal_the_lds_tiles(gpu, monkeypatch, name, t
 def test_eight_wave_tile_short_k_and_bf16_output(gpu, monkeypatch, name, type_id, k):
     """The 8-wave 64 x 64 tile (weight decode split by stage parity) at K of one and two blocks
     of 8 stages (the tail alone, one block switch) with a ragged last row tile: the bits of the
-    4-wave tile that shares activations through LDS, the f64 oracle, and a bf16 output equal to
-    the f32 result rounded."""
+    4-wave tile that shares activations through LDS and of the 4-wave register tile, the f64
+    oracle, and a bf16 output equal to the f32 result rounded."""
     n, m = 192, 70
     w, raw = make_matrix(gpu, type_id, n, k, seed=71)
     x, xv = activations("bf16", synth.normal_rows(72, m, k))
@@ -416,6 +416,13 @@ def test_eight_wave_tile_short_k_and_bf16_output(gpu, monkeypatch, name, type_id
         jq.matmul_plan(gpu, x, m, w, out, None, plan)
         outs[flag] = out
     assert torch.equal(outs["1"], outs["0"])
+    # the 4-wave register tile (the library's choice from two workgroups per CU) alike
+    monkeypatch.setenv("JV_GEMM_REG", "1")
+    monkeypatch.setenv("JV_GEMM_W8", "0")
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    jq.matmul_plan(gpu, x, m, w, out, None, plan)
+    assert torch.equal(outs["1"], out)
+    monkeypatch.delenv("JV_GEMM_W8")
     assert err(outs["1"].cpu().numpy(), oracle_product(type_id, raw, n, k, xv)) <= TOL
     monkeypatch.setenv("JV_GEMM_REG", "1")
     o16 = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
