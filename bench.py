@@ -122,9 +122,10 @@ class StreamProbe:
         self._ok(self.hip.hipModuleLaunchKernel(self.fn, grid, 1, 1, 512, 1, 1, 0, stream, args, None))
 
 
-def stream_floor(nbytes, copies, reps):
+def stream_floor(nbytes, copies, reps, pers=None):
     """Average duration (us) of one streaming read of `nbytes`, each launch on the next of
-    `copies` buffers (the products' weight rotation), for several bytes per workgroup."""
+    `copies` buffers (the products' weight rotation), for several bytes per workgroup (`pers`,
+    by default the four below)."""
     import torch
 
     probe = StreamProbe()
@@ -133,7 +134,7 @@ def stream_floor(nbytes, copies, reps):
     res = {}
     # one Q4_K tile (16 rows x 15 blocks, the M=1 kernel's workgroup), half and twice that, and
     # one range per compute unit
-    for per in (17280, 34560, 69120, (nbytes + 255) // 256 // 16 * 16 + 16):
+    for per in pers or (17280, 34560, 69120, (nbytes + 255) // 256 // 16 * 16 + 16):
         probe.launch(bufs[0], nbytes, per, sink)
         torch.cuda.synchronize()
         t = kernel_time_ms(lambda r, per=per: probe.launch(bufs[r % copies], nbytes, per, sink), reps)
@@ -390,8 +391,12 @@ def measure_configs(gpu, steps):
                       "fused_softcap_argmax_us": round((tf - t) * 1e3, 2),
                       "fused_total_us": round(tf * 1e3, 2)}
     del ms
+    # the floor of one plain streaming read of the same bytes (one copy exceeds the last-level
+    # cache): 16-byte loads, 17,280 and 69,120 bytes per workgroup
+    floor_lm = min(stream_floor(wbytes, 1, max(4, steps // 20), pers=(17280, 69120)).values())
     res["q6k_lm_head"] = {"workload": f"Q6_K vocabulary projection K={k} N={n} + per-row argmax, bf16 activations, f32 logits",
-                          "weight_bytes": wbytes, "per_m": lm}
+                          "weight_bytes": wbytes, "per_m": lm, "stream_floor_us": floor_lm,
+                          "stream_floor_GBps": round(wbytes / (floor_lm * 1e-6) / 1e9, 1)}
     log("q6k lm_head:", res["q6k_lm_head"])
     # expert-grouped product (MoE gate/up): 128 Q4_K experts [1408, 2816], 512 tokens routed to
     # 8 experts each (seeded uniform routing), grouped into jobs on the device
