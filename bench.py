@@ -430,8 +430,14 @@ def measure_configs(gpu, steps):
         cands[f"{bm}x{bn}"] = round(tc * 1e3, 2)
     t = cands[f"{pick[0]}x{pick[1]}"] * 1e-3
     tf = flops / (t * 1e-3) / 1e12
+    # the grouping of the same routes into the picked plan's jobs (jv_group_routes), written
+    # into the buffers of a first call
+    g = jq.group_routes(gpu, ids, experts, pick[0], in_div=top_k)
+    tg = kernel_time_ms(lambda r: jq.group_routes(gpu, ids, experts, pick[0], in_div=top_k, into=g),
+                        max(4, steps // 10))
     res["moe_grouped"] = {"workload": f"Q4_K expert-grouped product, {experts} experts N={n} K={k}, {tokens} tokens x top-{top_k}, "
                                       "jobs on the tuner's plan, bf16 activations, f32 out",
+                          "group_routes_us": round(tg * 1e3, 2),
                           "plan": {"bm": pick[0], "bn": pick[1]}, "kernel_us_by_plan": cands,
                           "kernel_us": round(t * 1e3, 2), "weight_bytes": raw.size,
                           "weight_GBps": round(raw.size / (t * 1e-3) / 1e9, 1),

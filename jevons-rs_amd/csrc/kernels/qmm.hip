@@ -2867,8 +2867,10 @@ extern "C" __global__ __launch_bounds__(1024) void jv_group_routes(const uint32_
     // A stable counting sort in one workgroup of NW waves. Wave w owns the contiguous
     // assignments [a0, a1): it counts them per expert, the counts become per-wave starting
     // positions (expert start + the counts of earlier waves), and the wave places its
-    // assignments in order, ranking the lanes of one expert within each 64-assignment batch by
-    // ballot. So every expert's positions hold its assignments in increasing order.
+    // assignments in order, ranking the lanes of one expert within each 64-assignment batch.
+    // So every expert's positions hold its assignments in increasing order. The lanes holding
+    // the same expert come from one ballot per bit of the expert id (same_expert), so a batch
+    // costs a fixed handful of instructions however many experts it touches.
     constexpr int NW = 16;
     __shared__ uint32_t cnt[NW][1024];
     __shared__ uint32_t starts[1025], jst[1025];
@@ -2877,12 +2879,23 @@ extern "C" __global__ __launch_bounds__(1024) void jv_group_routes(const uint32_
     __syncthreads();
     const uint32_t per = (assignments + NW - 1) / NW;
     const uint32_t a0 = min((uint32_t)wv * per, assignments), a1 = min(a0 + per, assignments);
+    // the lanes of this wave whose routed expert equals the lane's own (ex < experts)
+    auto same_expert = [&](uint32_t ex, bool todo) {
+        uint64_t same = __ballot(todo);
+        for (uint32_t b = 0; (1u << b) < experts; ++b) {  // wave-uniform
+            const bool bit = ((ex >> b) & 1u) != 0;
+            const uint64_t ones = __ballot(todo && bit);
+            same &= bit ? ones : ~ones;
+        }
+        return same;
+    };
     for (uint32_t c = a0; c < a1; c += 64) {
         const uint32_t a = c + (uint32_t)lane;
-        if (a < a1) {
-            const uint32_t ex = ids[a];
-            if (ex < experts) atomicAdd(&cnt[wv][ex], 1u);
-        }
+        const uint32_t ex = a < a1 ? ids[a] : 0xffffffffu;
+        const bool todo = ex < experts;
+        const uint64_t same = same_expert(ex, todo);
+        // the lowest lane of each expert adds the expert's count (one writer per entry)
+        if (todo && (same & ((1ull << lane) - 1)) == 0) cnt[wv][ex] += (uint32_t)__popcll(same);
     }
     __syncthreads();
     for (uint32_t ex = (uint32_t)tid; ex < experts; ex += 64 * NW) {  // counts -> wave prefixes
@@ -2943,20 +2956,14 @@ extern "C" __global__ __launch_bounds__(1024) void jv_group_routes(const uint32_
     for (uint32_t c = a0; c < a1; c += 64) {
         const uint32_t a = c + (uint32_t)lane;
         const uint32_t ex = a < a1 ? ids[a] : 0xffffffffu;
-        bool todo = ex < experts;
-        for (;;) {
-            const uint64_t active = __ballot(todo);
-            if (active == 0) break;
-            const int first = __ffsll((unsigned long long)active) - 1;
-            const uint32_t ef = (uint32_t)__shfl((int)ex, first);
-            const bool mine = todo && ex == ef;
-            const uint64_t same = __ballot(mine);
-            const uint32_t base = starts[ef] + cnt[wv][ef];
-            if (mine) {
-                sorted[base + (uint32_t)__popcll(same & ((1ull << lane) - 1))] = a;
-                todo = false;
-            }
-            if (lane == first) cnt[wv][ef] = cnt[wv][ef] + (uint32_t)__popcll(same);
+        const bool todo = ex < experts;
+        const uint64_t same = same_expert(ex, todo);
+        const uint32_t rank = (uint32_t)__popcll(same & ((1ull << lane) - 1));
+        uint32_t base = 0;
+        if (todo) base = starts[ex] + cnt[wv][ex];  // every lane reads before any lane writes
+        if (todo) {
+            sorted[base + rank] = a;
+            if (rank == 0) cnt[wv][ex] = base - starts[ex] + (uint32_t)__popcll(same);
         }
     }
 }

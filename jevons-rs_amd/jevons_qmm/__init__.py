@@ -402,16 +402,24 @@ class Groups:
                          self.in_div, self.rows)
 
 
-def group_routes(gpu: Gpu, ids, experts: int, bm: int, in_div: int = 1, stream=None) -> Groups:
+def group_routes(gpu: Gpu, ids, experts: int, bm: int, in_div: int = 1, stream=None,
+                 into: "Groups | None" = None) -> Groups:
     """ops::group_routes (crates/jevons-gemma4-diffusion/src/gpu/ops.rs:1100-1130): groups the
-    routed assignments `ids` (device int32 expert per assignment) by expert for row tiles of bm."""
+    routed assignments `ids` (device int32 expert per assignment) by expert for row tiles of bm.
+    `into`: the Groups of an earlier call with the same sizes, whose buffers are written again
+    (no allocation, e.g. under graph capture)."""
     import torch
 
     a = ids.numel()
     max_jobs = (a + bm - 1) // bm + experts
-    sorted_ = torch.zeros(max(a, 1), dtype=torch.int32, device=ids.device)
-    offsets = torch.zeros(experts + 1, dtype=torch.int32, device=ids.device)
-    jobs = torch.zeros(1 + 2 * max_jobs, dtype=torch.int32, device=ids.device)
+    if into is not None:
+        sorted_, offsets, jobs = into.ids, into.offsets, into.jobs
+        if sorted_.numel() != max(a, 1) or offsets.numel() != experts + 1 or jobs.numel() != 1 + 2 * max_jobs:
+            raise ValueError("group_routes: `into` was made for other sizes")
+    else:
+        sorted_ = torch.zeros(max(a, 1), dtype=torch.int32, device=ids.device)
+        offsets = torch.zeros(experts + 1, dtype=torch.int32, device=ids.device)
+        jobs = torch.zeros(1 + 2 * max_jobs, dtype=torch.int32, device=ids.device)
     _check(lib().jv_group_routes(gpu.handle, _dev(ids), a, experts, bm, _dev(sorted_), _dev(offsets),
                                  _dev(jobs), jobs.numel(), _stream(stream)))
     return Groups(sorted_, offsets, jobs, max_jobs, in_div, a)

@@ -608,6 +608,28 @@ def test_group_routes_match_the_oracle(gpu, experts, bm, a):
     assert g.ids.cpu().numpy().view(np.uint32)[:sorted_.size].tolist() == sorted_.tolist()
 
 
+def test_group_routes_far_ids_and_rewrites(gpu):
+    """Ids far past the expert count (any bit pattern) are not routed, and a second grouping of
+    other routes written into the first one's buffers (`into`) equals the oracle's."""
+    experts, bm, a = 100, 32, 3000
+    rng = np.random.default_rng(11)
+    ids = rng.integers(0, experts, a).astype(np.uint32)
+    ids[::7] = rng.integers(experts, 2**32, ids[::7].size, dtype=np.uint64).astype(np.uint32)
+    g = jq.group_routes(gpu, _i32(ids), experts, bm)
+    ids2 = rng.integers(0, experts, a).astype(np.uint32)
+    jq.group_routes(gpu, _i32(ids2), experts, bm, into=g)
+    for got, want in ((g, O.group_routes(ids2, experts, bm)),):
+        sorted_, offsets, jobs = want
+        njobs = int(jobs[0])
+        assert got.jobs.cpu().numpy().view(np.uint32)[:1 + 2 * njobs].tolist() == jobs[:1 + 2 * njobs].tolist()
+        assert got.offsets.cpu().numpy().view(np.uint32).tolist() == offsets.tolist()
+        assert got.ids.cpu().numpy().view(np.uint32)[:sorted_.size].tolist() == sorted_.tolist()
+    g1 = jq.group_routes(gpu, _i32(ids), experts, bm)
+    sorted_, offsets, jobs = O.group_routes(ids, experts, bm)
+    assert g1.offsets.cpu().numpy().view(np.uint32).tolist() == offsets.tolist()
+    assert g1.ids.cpu().numpy().view(np.uint32)[:sorted_.size].tolist() == sorted_.tolist()
+
+
 def test_grouped_products_use_each_assignments_expert_weights(gpu):
     """grouped_products_use_each_assignments_expert_weights (gpu/tests.rs:360-425): Q8_0
     weights of 4 experts (n=128, k=256), 21 tokens routed to 2 experts each, every grouped tile
