@@ -1489,7 +1489,7 @@ jv_status jv_softcap_logits(jv_ctx *ctx, float *x, size_t len, float cap, void *
     if (!x) return fail(JV_ERR_INVALID, "null buffer");
     int64_t n = (int64_t)len;
     void *args[] = {&x, &n, &cap};
-    return launch(ctx, "jv_softcap", dim3((unsigned)((len + 255) / 256)), dim3(256), 0, stream, args);
+    return launch(ctx, "jv_softcap", dim3((unsigned)((len + 1023) / 1024)), dim3(256), 0, stream, args);
 }
 
 jv_status jv_pick_logits(jv_ctx *ctx, const void *x, jv_act act, size_t x_len,

@@ -2799,10 +2799,22 @@ extern "C" __global__ __launch_bounds__(256) void jv_repack_q5_0(RepackParams p)
 // lm_head consumers (crates/jevons-gemma4-diffusion/src/gpu/ops.rs:589-634, :750-758).
 // ---------------------------------------------------------------------------------------------
 
-// In-place final-logit soft capping: x = cap tanh(x / cap).
+// In-place final-logit soft capping: x = cap tanh(x / cap). Thread t handles x[4t .. 4t + 3]:
+// one 16-byte load and store where x is 16-byte aligned, element by element otherwise and at
+// the end of the buffer.
 extern "C" __global__ __launch_bounds__(256) void jv_softcap(float *x, int64_t len, float cap) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < len) x[i] = soft_capped(x[i], cap);
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= len) return;
+    if (i + 4 <= len && ((uintptr_t)x & 15u) == 0) {
+        float4 v = *(const float4 *)(x + i);
+        v.x = soft_capped(v.x, cap);
+        v.y = soft_capped(v.y, cap);
+        v.z = soft_capped(v.z, cap);
+        v.w = soft_capped(v.w, cap);
+        *(float4 *)(x + i) = v;
+    } else {
+        for (int64_t j = i; j < len && j < i + 4; ++j) x[j] = soft_capped(x[j], cap);
+    }
 }
 
 // One workgroup per (row, token) pair: thread i covers K unit i / 4 and lane group i % 4 of the

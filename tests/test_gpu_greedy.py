@@ -185,3 +185,21 @@ def test_matmul_argmax_without_epilogue_kernels(gpu, kind, m):
         ref_out, ref_idx = _three_steps(gpu, x, m, w, n, cap, scratch)
         out, idx = _fused(gpu, x, m, w, n, cap, scratch)
         assert torch.equal(out, ref_out) and torch.equal(idx, ref_idx), cap
+
+
+def test_softcap_on_unaligned_and_ragged_buffers(gpu):
+    """The soft cap runs four values per thread, with 16-byte accesses where the buffer allows:
+    a buffer starting 4 bytes past that alignment, and lengths that are not a multiple of four,
+    give the same values as an aligned buffer, and nothing outside the buffer changes."""
+    v = np.random.default_rng(17).standard_normal(4099).astype(np.float32) * np.float32(50)
+    a = torch.from_numpy(v.copy()).cuda()
+    jq.softcap_logits(gpu, a, 30.0)
+    b = torch.from_numpy(np.concatenate([np.float32([123.0]), v, np.float32([456.0])])).cuda()
+    jq.softcap_logits(gpu, b[1:-1], 30.0)
+    assert torch.equal(a, b[1:-1])
+    assert float(b[0]) == 123.0 and float(b[-1]) == 456.0
+    for n in (1, 2, 3, 5, 7, 1026):
+        c = torch.from_numpy(np.concatenate([v[:n], np.float32([789.0])])).cuda()
+        jq.softcap_logits(gpu, c[:n], 30.0)
+        assert torch.equal(c[:n], a[:n]), n
+        assert float(c[n]) == 789.0, n
