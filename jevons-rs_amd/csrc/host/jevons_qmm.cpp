@@ -626,10 +626,13 @@ bool block_slices(const jv_qmatrix *w, uint32_t splits) {
     return true;
 }
 
+// Plans the pipelined tiles run (the others run the generic tiles): 256 x 128, 128 x 128 and
+// 64 x 64 in every format, 32 x 64 and 32 x 128 for the register-tile formats.
 bool pipelined_plan(const jv_qmatrix *w, jv_plan plan) {
     return w->k % 256 == 0 && block_slices(w, plan.splits) &&
            ((plan.bm == 256 && plan.bn == 128) || (plan.bm == 128 && plan.bn == 128) ||
-            (plan.bm == 64 && plan.bn == 64) || (reg_format(w) && plan.bm == 32 && plan.bn == 64));
+            (plan.bm == 64 && plan.bn == 64) ||
+            (reg_format(w) && plan.bm == 32 && (plan.bn == 64 || plan.bn == 128)));
 }
 
 // `scratch` holds the split-K partials (plans with splits > 1); when it is the fixed array of

@@ -2647,7 +2647,9 @@ __device__ __forceinline__ void gemm8_body(const GemmParams &p) {
 // on the 4 x 2 / 2 x 2 grid with each wave loading all of its m-tiles (APRIV, waves of one grid
 // row load the same fragments) and reading only its share of the weights from LDS. These three
 // formats also have a 32 x 64 r tile (2 x 2 waves of 16 x 32) for products of up to 32 rows,
-// which a 64-row tile would half fill.
+// which a 64-row tile would half fill, and a 32 x 128 r tile (2 x 2 waves of 16 x 64) for the
+// 32 x 128 plans (slower than 32 x 64, which the library's own plans take; faster than the
+// generic tiles that ran those plans).
 // Those are the library's tiles for these formats (the faster arrangement per format and tile
 // in interleaved measurements); the same bits either way. The last argument is how many VALU
 // instructions the scheduler places after each MFMA of a stage (the weight decode is spread
@@ -2678,6 +2680,9 @@ JV_GEMMP(q8_0, DF<FQ8_0>, 8, 8, 4, 2, 128, 128, r, 3)
 JV_GEMMP(q4k, DQ4K, 2, 4, 2, 2, 32, 64, r, 2)
 JV_GEMMP(q6k, DF<FQ6K>, 2, 4, 2, 2, 32, 64, r, 2)
 JV_GEMMP(q8_0, DF<FQ8_0Mix>, 2, 4, 2, 2, 32, 64, r, 2)
+JV_GEMMP(q4k, DQ4K, 2, 8, 2, 2, 32, 128, r, 2)
+JV_GEMMP(q6k, DF<FQ6K>, 2, 8, 2, 2, 32, 128, r, 2)
+JV_GEMMP(q8_0, DF<FQ8_0Mix>, 2, 8, 2, 2, 32, 128, r, 2)
 // The register tiles above with the greedy epilogue (vocabulary projections): the same
 // template arguments and a _g suffix.
 #define JV_GEMMG(NAME, D, TM, TN, WM, WN, ROWS, COLS, HB, APRIV, NV)                          \
@@ -2687,6 +2692,9 @@ JV_GEMMP(q8_0, DF<FQ8_0Mix>, 2, 4, 2, 2, 32, 64, r, 2)
 JV_GEMMG(q4k, DQ4K, 2, 4, 2, 2, 32, 64, true, true, 2)
 JV_GEMMG(q6k, DF<FQ6K>, 2, 4, 2, 2, 32, 64, true, true, 2)
 JV_GEMMG(q8_0, DF<FQ8_0Mix>, 2, 4, 2, 2, 32, 64, true, true, 2)
+JV_GEMMG(q4k, DQ4K, 2, 8, 2, 2, 32, 128, true, true, 2)
+JV_GEMMG(q6k, DF<FQ6K>, 2, 8, 2, 2, 32, 128, true, true, 2)
+JV_GEMMG(q8_0, DF<FQ8_0Mix>, 2, 8, 2, 2, 32, 128, true, true, 2)
 JV_GEMMG(q4k, DQ4K, 8, 8, 4, 2, 128, 128, true, true, 1)
 JV_GEMMG(q6k, DF<FQ6K>, 8, 8, 4, 2, 128, 128, true, true, 1)
 JV_GEMMG(q8_0, DF<FQ8_0>, 8, 8, 4, 2, 128, 128, true, true, 3)

@@ -582,7 +582,8 @@ def test_q4k_prefill_gemm_m512_rows(gpu):
     say("plan", plan, "normalized error", e)
     assert e <= TOL
     for r0 in (0, 200, 496):
-        for small in (jq.Plan(32, 64, 1), jq.Plan(32, 128, 1)):  # pipelined and generic tiles
+        # the 32 x 64 and 32 x 128 register tiles and the generic tiles (32 x 256)
+        for small in (jq.Plan(32, 64, 1), jq.Plan(32, 128, 1), jq.Plan(32, 256, 1)):
             o1 = torch.empty((16, n), dtype=torch.float32, device="cuda")
             jq.matmul_plan(gpu, x[r0:r0 + 16].contiguous(), 16, w, o1, None, small)
             assert torch.equal(o1, out[r0:r0 + 16]), (r0, small)
