@@ -509,11 +509,12 @@ jv_status launch_pack(jv_ctx *ctx, const void *x, jv_act act, size_t rows, size_
         return launch(ctx, "jv_pack_x", dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, args);
     }
     // a workgroup per P rows, of the fewest waves (at most 16) that keep every thread at 8 chunks
-    // or fewer: P = 1 for up to 256 rows of K <= 4096, 2 for up to 256 longer rows, else 4 (the
+    // or fewer: P = 1 for up to 512 rows of K <= 4096, 2 for up to 256 longer rows, else 4 (the
     // fastest of P = 1, 2, 4 per shape in kernel traces: M = 32 K = 3840 4.2 against 5.3 us,
-    // M = 256 K = 15360 11.6 against 14.4 us, M = 4096 K = 3840 11.6 against 16.0 us)
+    // M = 256 K = 15360 11.6 against 14.4 us, M = 4096 K = 3840 11.6 against 16.0 us; and on the
+    // M = 512 K = 3840 GEMM with its product, interleaved, 77.4 against 78.5 us with P = 4)
     const size_t packed_rows = rowmajor ? rows : (size_t)mtiles * 16;
-    const size_t P = packed_rows > 256 ? 4 : k <= 4096 ? 1 : 2;
+    const size_t P = k <= 4096 ? (packed_rows > 512 ? 4 : 1) : (packed_rows > 256 ? 4 : 2);
     const size_t chunks = k / 8;
     const size_t nw = std::min<size_t>(16, std::max<size_t>(4 / P, (chunks * P + 511) / 512));
     pk.rpw = (int32_t)P;
